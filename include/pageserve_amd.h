@@ -1,0 +1,131 @@
+/*
+ * pageserve_amd: C ABI of the MI355X (gfx950) INT8 weight-only linear path.
+ *
+ * Every entry point takes plain device pointers, element counts and an opaque
+ * hipStream_t (passed as void*; NULL means the default stream).  All launches
+ * are asynchronous on that stream; no entry point synchronises the host and
+ * none allocates device memory.  Buffers are owned by the caller.
+ *
+ * Return value: PGS_OK (0) or one of the PGS_ERR_* codes below.  A call that
+ * returns an error has launched nothing.  pgs_last_error() gives a
+ * human-readable message for the calling thread's most recent failure.
+ *
+ * Layouts (row-major, densely packed, no leading-dimension argument):
+ *   weight w   [n, k]  fp32 or bf16   (out_features, in_features)
+ *   q          [n, k]  int8           per-output-row symmetric quantization
+ *   scale      [n]     fp32           (the reference stores it as [n, 1])
+ *   x          [m, k]  bf16           activations
+ *   bias       [n]     bf16           optional (NULL = none)
+ *   y          [m, n]  bf16 or fp32   y = x . (q * scale)^T + bias
+ *
+ * Reference interface (Rakshit-gen/pageserve, a Python package with no FFI):
+ * each entry point below names the Python function or call site it replaces.
+ */
+#ifndef PAGESERVE_AMD_H
+#define PAGESERVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type codes */
+#define PGS_DTYPE_F32 0
+#define PGS_DTYPE_BF16 1
+#define PGS_DTYPE_F16 2
+
+/* return codes */
+#define PGS_OK 0
+#define PGS_ERR_INVALID_ARGUMENT 1 /* bad size, null pointer, bad dtype code */
+#define PGS_ERR_MISALIGNED 2       /* pointer not aligned to its element size */
+#define PGS_ERR_LAUNCH 3           /* the HIP runtime rejected a kernel launch */
+#define PGS_ERR_NO_DEVICE 4        /* no usable gfx950 device */
+
+/* ABI version: bumped whenever a signature below changes. */
+int pgs_abi_version(void);
+
+/* Static string for a return code. */
+const char* pgs_error_string(int code);
+
+/* Detail of the calling thread's most recent failed call ("" if none). */
+const char* pgs_last_error(void);
+
+/*
+ * Replaces quantize_per_channel(weight) -- engine/quantization.py:16-23.
+ *   absmax[r] = max(max_j |w[r,j]|, 1e-8f)
+ *   scale[r]  = absmax[r] / 127.0f                 (IEEE fp32 division)
+ *   q[r,j]    = clamp(rint(w[r,j] / scale[r]), -127, 127)   (ties to even)
+ * Bit-exact with the reference's CPU arithmetic.  w_dtype: PGS_DTYPE_F32 or
+ * PGS_DTYPE_BF16 (a bf16 weight widens exactly, as weight.float() does).
+ * Non-finite weights give unspecified q/scale, as in the reference.
+ */
+int pgs_quantize_per_channel(const void* w, int w_dtype, int64_t n, int64_t k,
+                             int8_t* q, float* scale, void* stream);
+
+/*
+ * Replaces dequantize(q, scale, dtype) -- engine/quantization.py:26-27.
+ *   out[r,j] = dtype(float(q[r,j]) * scale[r])  (fp32 product, then one
+ *   round-to-nearest-even conversion to out_dtype).  Bit-exact.
+ * out_dtype: PGS_DTYPE_F32, PGS_DTYPE_BF16 or PGS_DTYPE_F16.
+ */
+int pgs_dequantize(const int8_t* q, const float* scale, int64_t n, int64_t k,
+                   void* out, int out_dtype, void* stream);
+
+/*
+ * Replaces F.linear(x, _resolve(W), b) for a QuantizedWeight W --
+ * engine/model.py:25-26 (_resolve -> QuantizedWeight.get -> dequantize) feeding
+ * the projections at engine/model.py:168-170 (q/k/v, with bias), :184 (o),
+ * :188-190 (gate, up, down) and, with y_dtype = PGS_DTYPE_F32, the lm_head
+ * at engine/model.py:193.
+ *   y[i,r] = sum_j x[i,j] * q[r,j] * scale[r] (+ bias[r]),  fp32 accumulate.
+ * The dense weight is never materialised.  y_dtype: PGS_DTYPE_BF16 or
+ * PGS_DTYPE_F32.  Dispatches on m: the skinny kernel for m <= 16, the
+ * MFMA tile kernel above.
+ */
+int pgs_w8a16_linear(const void* x, const int8_t* q, const float* scale,
+                     const void* bias, void* y, int y_dtype, int64_t m,
+                     int64_t n, int64_t k, void* stream);
+
+/*
+ * One output of a grouped linear: several quantized weights that read the
+ * same activations (the q/k/v triple of engine/model.py:168-170).
+ */
+typedef struct pgs_linear_out {
+  const int8_t* q;     /* [n, k] int8 */
+  const float* scale;  /* [n] fp32 */
+  const void* bias;    /* [n] bf16 or NULL */
+  void* y;             /* [m, n] of y_dtype */
+  int64_t n;           /* rows of this weight */
+} pgs_linear_out;
+
+#define PGS_MAX_GROUP 4
+
+/*
+ * Replaces the three F.linear calls of engine/model.py:168-170 (q, k, v
+ * projections of the same normalised hidden state) with one launch.  Each
+ * output is exactly what pgs_w8a16_linear would write for it.
+ * 1 <= n_outs <= PGS_MAX_GROUP.
+ */
+int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
+                           int n_outs, int y_dtype, int64_t m, int64_t k,
+                           void* stream);
+
+/*
+ * Replaces gate = F.linear(h, Wg); up = F.linear(h, Wu); F.silu(gate) * up
+ * -- engine/model.py:188-190 -- with one fused launch:
+ *   act[i,r] = silu(g) * u,  g = sum_j x[i,j] q_gate[r,j] * s_gate[r],
+ *                            u = sum_j x[i,j] q_up[r,j] * s_up[r]
+ * computed in fp32 and rounded once to bf16.  act: bf16 [m, n].
+ * The down projection is a separate pgs_w8a16_linear call on act.
+ */
+int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float* s_gate,
+                     const int8_t* q_up, const float* s_up, void* act,
+                     int64_t m, int64_t n, int64_t k, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGESERVE_AMD_H */

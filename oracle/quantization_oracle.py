@@ -1,0 +1,207 @@
+"""numpy restatement of pageserve's INT8 weight-only quantization arithmetic.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the checker the HIP
+kernels are compared against, never part of the product.
+
+Reference: Rakshit-gen/pageserve ``engine/quantization.py`` and the call sites
+in ``engine/model.py``.  The reference runs these ops with PyTorch on the CPU;
+the semantics restated here are:
+
+* ``Tensor.float()``: exact widening (bf16 -> fp32 is a 16-bit shift).
+* ``abs().amax(dim=1)``: exact (a max is order independent).
+* ``clamp(min=1e-8)``: the Python scalar becomes ``float32(1e-8)``.
+* ``absmax / 127.0`` and ``weight / scale``: IEEE-754 fp32 division, correctly
+  rounded (no reciprocal multiply).
+* ``round()``: round half to even.
+* ``clamp(-127, 127).to(int8)``: saturate to the symmetric range.
+* ``.to(bfloat16)``: round to nearest even.
+
+Pinning (tests/test_oracle_pins.py): the quantizer is checked against an
+independent exact-rational computation (``fractions.Fraction`` quotients
+rounded to fp32 by hand, Python's own ties-to-even ``round``) on hand-built
+known-answer rows and random matrices; the matmul against exact rational dot
+products; each against a list of planted mistakes that must fail.  The
+reference itself holds no golden vectors, only the bounds of
+``tests/test_quantization.py:14-46``, which are re-asserted here too.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+EPS_ABSMAX = F32(1e-8)  # engine/quantization.py:20  .clamp(min=1e-8)
+QMAX = F32(127.0)       # engine/quantization.py:21  absmax / 127.0
+
+
+# --------------------------------------------------------------------------
+# bf16 helpers (numpy has no bfloat16; bf16 values travel as uint16 bits)
+# --------------------------------------------------------------------------
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """Exact widening of bf16 bit patterns (uint16) to float32."""
+    b = np.asarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even; NaN -> canonical quiet NaN.
+
+    Matches torch's ``Tensor.to(torch.bfloat16)`` on finite inputs.
+    """
+    f = np.ascontiguousarray(x, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    rounded = (u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)
+    out = rounded.astype(np.uint16)
+    nan = np.isnan(f)
+    if nan.any():
+        out = np.where(nan, np.uint16(0x7FC0), out)
+    return out
+
+
+def round_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 values rounded to the nearest bf16 value (returned as float32)."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+# --------------------------------------------------------------------------
+# a1: quantize_per_channel  (engine/quantization.py:16-23)
+# --------------------------------------------------------------------------
+
+def quantize_per_channel(weight: np.ndarray, *, bf16_bits: bool = False):
+    """Returns ``(q int8 [N,K], scale float32 [N,1])``.
+
+    ``weight``: float32 ``[N,K]``, or uint16 bf16 bit patterns when
+    ``bf16_bits`` is true.  Follows engine/quantization.py:20-23 op by op.
+    """
+    w = bf16_bits_to_f32(weight) if bf16_bits else np.asarray(weight, dtype=np.float32)
+    if w.ndim != 2:
+        raise ValueError("weight must be 2-D (out_features, in_features)")
+    # :20  absmax = weight.float().abs().amax(dim=1, keepdim=True).clamp(min=1e-8)
+    if w.shape[1] == 0:
+        absmax = np.full((w.shape[0], 1), EPS_ABSMAX, dtype=np.float32)
+    else:
+        absmax = np.abs(w).max(axis=1, keepdims=True)
+        absmax = np.maximum(absmax, EPS_ABSMAX)  # NaN propagates, as clamp does
+    # :21  scale = absmax / 127.0      (fp32 / fp32, IEEE)
+    scale = (absmax / QMAX).astype(np.float32)
+    # :22  q = clamp((weight.float() / scale).round(), -127, 127).to(int8)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = (w / scale).astype(np.float32)
+    q = np.clip(np.rint(ratio), F32(-127.0), F32(127.0))
+    q = np.nan_to_num(q, nan=0.0).astype(np.int8)  # NaN: unspecified in the reference
+    return q, scale
+
+
+# --------------------------------------------------------------------------
+# a2: dequantize  (engine/quantization.py:26-27)
+# --------------------------------------------------------------------------
+
+def dequantize(q: np.ndarray, scale: np.ndarray, dtype: str = "f32") -> np.ndarray:
+    """``(q.to(float32) * scale).to(dtype)``.
+
+    dtype "f32" -> float32 array; "bf16" -> uint16 bf16 bits; "f16" -> float16.
+    """
+    prod = (np.asarray(q).astype(np.float32) * np.asarray(scale, dtype=np.float32).reshape(-1, 1)).astype(np.float32)
+    if dtype == "f32":
+        return prod
+    if dtype == "bf16":
+        return f32_to_bf16_bits(prod)
+    if dtype == "f16":
+        return prod.astype(np.float16)
+    raise ValueError(f"unknown dtype {dtype!r}")
+
+
+# --------------------------------------------------------------------------
+# a5-a8: the fp32 dequant-and-matmul (engine/model.py:168-170,184,188-190,193)
+# --------------------------------------------------------------------------
+
+def linear(x: np.ndarray, q: np.ndarray, scale: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """fp32 oracle of ``F.linear(x, dequantize(q, scale, float32), bias)``.
+
+    ``x``: float32 ``[M,K]`` (activation values, already bf16-representable in
+    the GPU workloads).  ``bias``: float32 ``[N]`` or None.  The dequantized
+    weight is formed in fp32 exactly as engine/quantization.py:27 forms it; the
+    sum runs in float64 so the oracle is deterministic (BLAS fp32 results vary
+    with blocking and thread count) and is then rounded to float32.
+    """
+    w = dequantize(q, scale, "f32").astype(np.float64)
+    y = np.asarray(x, dtype=np.float64) @ w.T
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float64).reshape(1, -1)
+    return y.astype(np.float32)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """``F.silu``: x * sigmoid(x), in float64."""
+    x = np.asarray(x, dtype=np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def swiglu(x, q_gate, s_gate, q_up, s_up) -> np.ndarray:
+    """``F.silu(F.linear(h, Wg)) * F.linear(h, Wu)`` (engine/model.py:188-190), fp32."""
+    g = linear(x, q_gate, s_gate).astype(np.float64)
+    u = linear(x, q_up, s_up).astype(np.float64)
+    return (silu(g) * u).astype(np.float32)
+
+
+def mlp(x, q_gate, s_gate, q_up, s_up, q_down, s_down) -> np.ndarray:
+    """``F.linear(F.silu(gate) * up, Wd)`` (engine/model.py:188-190) in fp32 throughout."""
+    act = swiglu(x, q_gate, s_gate, q_up, s_up)
+    return linear(act, q_down, s_down)
+
+
+# --------------------------------------------------------------------------
+# Tolerances stated by the path's specification
+# --------------------------------------------------------------------------
+
+REL_TOL = 1e-2  # max|y - y_ref| / max|y_ref|   (tests/test_quantization.py:45 definition)
+
+
+def abs_tol(k: int) -> float:
+    """Max elementwise abs error allowed for a reduction of length k."""
+    return 2e-2 * float(np.sqrt(k / 1024.0))
+
+
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at |v| (8 significant bits)."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False) -> dict:
+    """Error report of y against the oracle; ``ok`` when both bounds hold.
+
+    ``rel`` = max|y - y_ref| / max|y_ref| must be <= 1e-2 and every element
+    must satisfy |y - y_ref| <= 2e-2 * sqrt(k/1024).  For a bf16 output
+    (``bf16_out``) the elementwise bound is floored at one bf16 ulp of the
+    reference value: below that spacing no bf16 result can resolve the bound
+    (a value in [8, 16) already has a half-ulp of 0.031 > 2e-2 * sqrt(2)).
+    """
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(y_ref, dtype=np.float64)
+    if y.shape != r.shape:
+        raise ValueError(f"shape mismatch {y.shape} vs {r.shape}")
+    tol = abs_tol(k)
+    if y.size == 0:
+        return {"max_abs": 0.0, "rel": 0.0, "abs_tol": tol, "ok": True}
+    diff = np.abs(y - r)
+    max_abs = float(diff.max())
+    denom = float(np.abs(r).max())
+    rel = max_abs / denom if denom > 0 else max_abs
+    bound = np.maximum(tol, bf16_ulp(r)) if bf16_out else tol
+    worst = float((diff / bound).max())
+    ok = bool(np.isfinite(y).all()) and rel <= REL_TOL and worst <= 1.0
+    return {"max_abs": max_abs, "rel": rel, "abs_tol": tol, "worst_vs_bound": worst, "ok": ok}
+
+
+def argmax_rows(logits: np.ndarray) -> np.ndarray:
+    """First index of the row maximum (torch.argmax tie rule), per row."""
+    return np.argmax(np.asarray(logits), axis=-1)
+
+
+def top2_gap(logits: np.ndarray) -> np.ndarray:
+    """Per-row gap between the largest and second-largest logit."""
+    part = np.partition(np.asarray(logits, dtype=np.float64), -2, axis=-1)
+    return part[..., -1] - part[..., -2]

@@ -1,0 +1,19 @@
+"""pageserve_amd: MI355X (gfx950) INT8 weight-only linear path.
+
+A drop-in for pageserve's ``engine/quantization.py``: the same Python API,
+computed by hand-written HIP kernels behind a C ABI
+(``include/pageserve_amd.h``).
+"""
+
+from .quantization import (  # noqa: F401
+    QuantizedWeight,
+    W8A16Weight,
+    dequantize,
+    linear,
+    linear_group,
+    mlp,
+    quantize_per_channel,
+    swiglu,
+)
+
+__version__ = "0.1.0"

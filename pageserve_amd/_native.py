@@ -1,0 +1,110 @@
+"""ctypes binding of the gfx950 C-ABI library (``include/pageserve_amd.h``).
+
+The library is built in-tree by ``pageserve_amd.build`` into
+``pageserve_amd/_lib/libpageserve_amd.so``.  Nothing here falls back to
+another implementation: if the library is missing or cannot be loaded, every
+entry point raises :class:`NativeLibraryError`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(os.environ.get("PAGESERVE_AMD_LIB", Path(__file__).resolve().parent / "_lib" / "libpageserve_amd.so"))
+HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "pageserve_amd.h"
+
+# element type codes and return codes (include/pageserve_amd.h)
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+OK = 0
+MAX_GROUP = 4
+ABI_VERSION = 1
+
+
+class NativeLibraryError(RuntimeError):
+    """The gfx950 library is missing, stale or failed a call."""
+
+
+class LinearOut(ctypes.Structure):
+    """``pgs_linear_out`` of include/pageserve_amd.h."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+    ]
+
+
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+
+# name -> (restype, argtypes); every symbol the header declares
+SIGNATURES = {
+    "pgs_abi_version": (_INT, []),
+    "pgs_error_string": (ctypes.c_char_p, [_INT]),
+    "pgs_last_error": (ctypes.c_char_p, []),
+    "pgs_quantize_per_channel": (_INT, [_VP, _INT, _I64, _I64, _VP, _VP, _VP]),
+    "pgs_dequantize": (_INT, [_VP, _VP, _I64, _I64, _VP, _INT, _VP]),
+    "pgs_w8a16_linear": (_INT, [_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP]),
+    "pgs_w8a16_linear_group": (_INT, [_VP, ctypes.POINTER(LinearOut), _INT, _INT, _I64, _I64, _VP]),
+    "pgs_w8a16_swiglu": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def header_symbols(path: Path = HEADER_PATH) -> list[str]:
+    """Function names declared in the public header."""
+    text = path.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pgs_[a-z0-9_]+)\s*\(", text)))
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Loads (once) and returns the library with typed entry points."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise NativeLibraryError(
+                f"pageserve_amd: gfx950 library not found at {p}; build it with "
+                "`python -m pageserve_amd.build` (there is no fallback implementation)"
+            )
+        try:
+            lib = ctypes.CDLL(str(p))
+        except OSError as e:
+            raise NativeLibraryError(f"pageserve_amd: cannot load {p}: {e}") from e
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.pgs_abi_version()
+        if ver != ABI_VERSION:
+            raise NativeLibraryError(f"pageserve_amd: library ABI {ver} != expected {ABI_VERSION}; rebuild it")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raises on a non-zero return code, with the library's own message."""
+    if rc == OK:
+        return
+    lib = load()
+    detail = lib.pgs_last_error().decode(errors="replace")
+    kind = lib.pgs_error_string(rc).decode(errors="replace")
+    exc = ValueError if rc in (1, 2) else NativeLibraryError
+    raise exc(f"{what}: {kind}: {detail}")

@@ -1,0 +1,92 @@
+"""Builds the gfx950 shared library ``pageserve_amd/_lib/libpageserve_amd.so``.
+
+``python -m pageserve_amd.build`` (or ``build()``) compiles every ``csrc/*.hip``
+with hipcc for gfx950 and links them into one C-ABI shared library that the
+Python host code loads with ctypes.  hipcc cross-compiles, so this runs on a
+machine without a GPU.
+
+Flags that matter for results:
+* no fast-math, and ``-fhip-fp32-correctly-rounded-divide-sqrt``: the
+  quantizer's ``w / scale`` must be a correctly rounded IEEE division;
+* ``-packed-fp32-ops`` off: packed fp32 VALU forms are not emitted.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+LIBDIR = PKG / "_lib"
+LIBNAME = "libpageserve_amd.so"
+OBJDIR = ROOT / "_build" / "obj"
+
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _compile(hipcc: str, src: Path) -> Path:
+    OBJDIR.mkdir(parents=True, exist_ok=True)
+    obj = OBJDIR / (src.stem + ".o")
+    cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    noise = "is not a recognized feature for this target"
+    warn = "\n".join(l for l in res.stderr.splitlines() if noise not in l and l.strip())
+    if warn:
+        print(f"[pageserve_amd.build] {src.name}:\n{warn}", file=sys.stderr)
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compiles and links the library; returns its path.  Always rebuilds."""
+    hipcc = _hipcc()
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(lambda s: _compile(hipcc, s), srcs))
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    out = LIBDIR / LIBNAME
+    tmp = LIBDIR / (LIBNAME + ".tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"[pageserve_amd.build] built {out} from {len(srcs)} sources for {ARCH}")
+    return out
+
+
+if __name__ == "__main__":
+    build()

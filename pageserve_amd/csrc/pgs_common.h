@@ -1,0 +1,74 @@
+// Shared device types, conversions and host-side error plumbing for the
+// gfx950 INT8 weight-only linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pageserve_amd.h"
+
+namespace pgs {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// conversions
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// 8 signed bytes (two dwords) -> 8 bf16, exact (|q| <= 127 fits bf16's 8-bit
+// significand).  Compiles to 8 v_cvt_f32_i32 with SDWA byte sign-extension
+// plus 4 v_cvt_pk_bf16_f32.
+__device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  f32x8 f = {(float)(int8_t)(lo), (float)(int8_t)(lo >> 8),
+             (float)(int8_t)(lo >> 16), (float)(int8_t)(lo >> 24),
+             (float)(int8_t)(hi), (float)(int8_t)(hi >> 8),
+             (float)(int8_t)(hi >> 16), (float)(int8_t)(hi >> 24)};
+  return __builtin_convertvector(f, bf16x8);
+}
+
+// fp32 -> bf16 bits, round to nearest even (hardware v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// x * sigmoid(x) in fp32 (F.silu).  expf is the device library's full
+// precision exponential.
+__device__ __forceinline__ float silu_f32(float x) {
+  return x / (1.0f + expf(-x));
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// host-side error handling (defined in pgs_api.hip)
+// ---------------------------------------------------------------------------
+
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+}  // namespace pgs

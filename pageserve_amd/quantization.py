@@ -1,0 +1,381 @@
+"""INT8 weight-only quantization with the interface of pageserve's
+``engine/quantization.py``, computed by gfx950 HIP kernels.
+
+Same names, argument meaning and return types as the reference:
+
+* ``quantize_per_channel(weight) -> (q int8 [N,K], scale fp32 [N,1])``
+  (engine/quantization.py:16-23), bit-identical to the reference's CPU result;
+* ``dequantize(q, scale, dtype)`` (engine/quantization.py:26-27), bit-identical;
+* ``QuantizedWeight(weight)`` with ``.dtype .q .scale .get() .to(device)
+  .storage_bytes`` (engine/quantization.py:30-50).
+
+What changes is the per-call path.  The reference's ``get()`` dequantizes the
+whole weight on every access and ``engine/model.py`` then runs a dense GEMM.
+Here ``get()`` on a GPU weight returns a :class:`W8A16Weight`, a tensor
+subclass of the same shape and dtype whose ``F.linear`` runs the fused W8A16
+kernel (int8 read once, scale and bias in the epilogue), so
+``F.linear(h, _resolve(w), b)`` in an unchanged ``engine/model.py`` takes the
+fused path.  Any other operation on it materialises the dense weight through
+the dequantize kernel, which is exactly what the reference's ``get()`` returns.
+
+Explicit entry points that the reference's call sites can use directly:
+``QuantizedWeight.linear``, :func:`linear_group` (q/k/v in one launch) and
+:func:`swiglu` (gate/up/silu*up in one launch, engine/model.py:188-190).
+
+Device placement follows the reference: results live where the input lives.
+All arithmetic runs on the GPU; a CPU-resident weight is staged to the current
+GPU for the kernel and the result copied back.  Without a GPU or without the
+built library every entry point raises (there is no CPU implementation).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _native
+from ._native import DTYPE_BF16, DTYPE_F16, DTYPE_F32, LinearOut, check
+
+__all__ = [
+    "quantize_per_channel",
+    "dequantize",
+    "QuantizedWeight",
+    "W8A16Weight",
+    "linear",
+    "linear_group",
+    "swiglu",
+    "mlp",
+]
+
+_DTYPE_CODE = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+
+
+# ---------------------------------------------------------------------------
+# plumbing
+# ---------------------------------------------------------------------------
+
+def _require_gpu() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "pageserve_amd: no ROCm GPU is visible; the INT8 linear path runs only on the "
+            "gfx950 HIP kernels (there is no CPU implementation)"
+        )
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class _on_device:
+    """Makes ``device`` current for the launch (cheap when it already is)."""
+
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, device: torch.device):
+        self.dev = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.dev:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _aligned(t: torch.Tensor, n: int = 16) -> torch.Tensor:
+    """Contiguous, with data pointer aligned to ``n`` bytes (copies only if needed)."""
+    t = t.contiguous()
+    if t.numel() and t.data_ptr() % n:
+        t = t.clone()
+    return t
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None and t.numel() else 0)
+
+
+# ---------------------------------------------------------------------------
+# quantize_per_channel / dequantize
+# ---------------------------------------------------------------------------
+
+def quantize_per_channel(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """weight: (out_features, in_features).  Returns (int8_weight, scale),
+    scale shape (out_features, 1), such that dequantize(int8_weight, scale)
+    ~= weight.  engine/quantization.py:16-23, bit-identical.
+    """
+    if not isinstance(weight, torch.Tensor):
+        raise TypeError("weight must be a torch.Tensor")
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D (out_features, in_features), got shape {tuple(weight.shape)}")
+    n, k = weight.shape
+    if k == 0 and n > 0:
+        # torch's amax refuses an empty reduction dimension; so does the reference
+        raise RuntimeError("amax(): Expected reduction dim 1 to have non-zero size.")
+    home = weight.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    w = weight
+    if w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.float()  # the reference's own first step, weight.float()
+    w = _aligned(w.to(dev, non_blocking=False))
+    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+    scale = torch.empty((n, 1), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_quantize_per_channel(
+            _ptr(w), _DTYPE_CODE[w.dtype], n, k, _ptr(q), _ptr(scale), _stream(dev)
+        )
+    check(rc, "quantize_per_channel")
+    if home.type != "cuda":
+        q, scale = q.to(home), scale.to(home)
+    return q, scale
+
+
+def dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``(q.to(float32) * scale).to(dtype)`` -- engine/quantization.py:26-27,
+    bit-identical.  ``scale``: per-row, shape (N, 1) or (N,).
+    """
+    if q.dim() != 2 or q.dtype != torch.int8:
+        raise ValueError("q must be a 2-D int8 tensor")
+    n, k = q.shape
+    if scale.numel() != n:
+        raise ValueError(f"scale must hold one value per row ({n}), got shape {tuple(scale.shape)}")
+    home = q.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    kdt = dtype if dtype in _DTYPE_CODE else torch.float32
+    qd = _aligned(q.to(dev))
+    sd = _aligned(scale.to(dev, dtype=torch.float32).reshape(n))
+    out = torch.empty((n, k), dtype=kdt, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_dequantize(_ptr(qd), _ptr(sd), n, k, _ptr(out), _DTYPE_CODE[kdt], _stream(dev))
+    check(rc, "dequantize")
+    if kdt != dtype:
+        out = out.to(dtype)  # fp32 product, then the reference's .to(dtype)
+    return out.to(home) if home.type != "cuda" else out
+
+
+# ---------------------------------------------------------------------------
+# fused linears
+# ---------------------------------------------------------------------------
+
+def _check_x(x: torch.Tensor, k: int, device: torch.device, what: str) -> torch.Tensor:
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{what}: input must be a torch.Tensor")
+    if x.device != device:
+        raise ValueError(f"{what}: input on {x.device} but weight on {device}")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: the W8A16 kernels take bf16 activations, got {x.dtype}")
+    if x.shape[-1] != k:
+        raise ValueError(f"{what}: input has {x.shape[-1]} features, weight expects {k}")
+    return _aligned(x.reshape(-1, k))
+
+
+def _check_bias(bias: torch.Tensor | None, n: int, device: torch.device, what: str) -> torch.Tensor | None:
+    if bias is None:
+        return None
+    if bias.device != device or bias.dtype != torch.bfloat16 or bias.numel() != n:
+        raise ValueError(f"{what}: bias must be a bf16 [{n}] tensor on {device}")
+    return _aligned(bias.reshape(n), 2)
+
+
+def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
+           out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """``F.linear(x, dequantize(q, scale, bf16), bias)`` fused: y = x (q s)^T + b.
+
+    x: bf16 [..., K] on the weight's GPU.  out_dtype: bf16 (projections) or
+    fp32 (the lm_head logits).  Returns [..., N].
+    """
+    return linear_group(x, [weight], [bias], out_dtype=out_dtype)[0]
+
+
+def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list | None = None,
+                 out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
+    """Several projections of the same input in one launch (q/k/v,
+    engine/model.py:168-170).  Returns one output per weight."""
+    if not weights or len(weights) > _native.MAX_GROUP:
+        raise ValueError(f"linear_group takes 1..{_native.MAX_GROUP} weights")
+    biases = list(biases) if biases is not None else [None] * len(weights)
+    if len(biases) != len(weights):
+        raise ValueError("one bias (or None) per weight")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
+    w0 = weights[0]
+    dev = w0.q.device
+    if dev.type != "cuda":
+        raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
+    k = w0.q.shape[1]
+    for w in weights:
+        if w.q.device != dev or w.q.shape[1] != k:
+            raise ValueError("linear_group: weights must share device and in_features")
+    lead = x.shape[:-1]
+    x2 = _check_x(x, k, dev, "linear")
+    m = x2.shape[0]
+    lib = _native.load()
+    outs = (LinearOut * len(weights))()
+    ys, keep = [], []
+    for i, (w, b) in enumerate(zip(weights, biases)):
+        n = w.q.shape[0]
+        bb = _check_bias(b, n, dev, "linear")
+        y = torch.empty((m, n), dtype=out_dtype, device=dev)
+        q, s = w._kernel_operands()
+        keep.extend([q, s, bb])
+        outs[i].q = q.data_ptr() if q.numel() else None
+        outs[i].scale = s.data_ptr() if s.numel() else None
+        outs[i].bias = bb.data_ptr() if bb is not None else None
+        outs[i].y = y.data_ptr() if y.numel() else None
+        outs[i].n = n
+        ys.append(y)
+    with _on_device(dev):
+        rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, _stream(dev))
+    check(rc, "w8a16 linear")
+    return [y.reshape(*lead, y.shape[1]) for y in ys]
+
+
+def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> torch.Tensor:
+    """``F.silu(F.linear(x, gate)) * F.linear(x, up)`` in one launch
+    (engine/model.py:188-190); fp32 inside, one rounding to bf16."""
+    dev = gate.q.device
+    if dev.type != "cuda" or up.q.device != dev:
+        raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
+    if gate.q.shape != up.q.shape:
+        raise ValueError("swiglu: gate and up weights must have the same shape")
+    n, k = gate.q.shape
+    lead = x.shape[:-1]
+    x2 = _check_x(x, k, dev, "swiglu")
+    m = x2.shape[0]
+    act = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    qg, sg = gate._kernel_operands()
+    qu, su = up._kernel_operands()
+    lib = _native.load()
+    with _on_device(dev):
+        rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, _stream(dev))
+    check(rc, "w8a16 swiglu")
+    return act.reshape(*lead, n)
+
+
+def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "QuantizedWeight") -> torch.Tensor:
+    """``F.linear(F.silu(gate(x)) * up(x), down)`` (engine/model.py:188-190, without
+    the residual add): the fused gate/up kernel, then the down projection."""
+    return linear(swiglu(x, gate, up), down)
+
+
+# ---------------------------------------------------------------------------
+# QuantizedWeight and the drop-in tensor view
+# ---------------------------------------------------------------------------
+
+class QuantizedWeight:
+    """Drop-in replacement for a plain weight tensor: stores int8 + scale
+    (engine/quantization.py:30-50).  ``get()`` gives a tensor that behaves as
+    the dequantized weight; ``F.linear`` on it runs the fused W8A16 kernel."""
+
+    def __init__(self, weight: torch.Tensor):
+        self.dtype = weight.dtype
+        self.q, self.scale = quantize_per_channel(weight)
+
+    def get(self) -> torch.Tensor:
+        if self.q.device.type == "cuda":
+            return W8A16Weight(self)
+        return dequantize(self.q, self.scale, self.dtype)
+
+    def to(self, device) -> "QuantizedWeight":
+        self.q = self.q.to(device)
+        self.scale = self.scale.to(device)
+        return self
+
+    @property
+    def storage_bytes(self) -> int:
+        return self.q.numel() * self.q.element_size() + self.scale.numel() * self.scale.element_size()
+
+    @property
+    def shape(self) -> torch.Size:
+        return self.q.shape
+
+    def dense(self) -> torch.Tensor:
+        """The reference's ``get()``: the dequantized weight in ``self.dtype``."""
+        return dequantize(self.q, self.scale, self.dtype)
+
+    def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        return linear(x, self, bias, out_dtype=out_dtype)
+
+    def _kernel_operands(self) -> tuple[torch.Tensor, torch.Tensor]:
+        q = self.q
+        if not q.is_contiguous() or (q.numel() and q.data_ptr() % 16):
+            q = _aligned(q)
+        s = self.scale.reshape(-1)
+        if s.dtype != torch.float32 or not s.is_contiguous():
+            s = s.to(torch.float32).contiguous()
+        return q, s
+
+
+class W8A16Weight(torch.Tensor):
+    """The value of ``QuantizedWeight.get()`` on a GPU.
+
+    Shape, dtype and device of the dense weight, but no dense storage.
+    ``F.linear(x, w, b)`` with bf16 ``x`` runs the fused W8A16 kernel; every
+    other operation (and ``F.linear`` on other activation dtypes) receives the
+    dense weight produced by the dequantize kernel, i.e. the reference's
+    ``get()`` result.
+    """
+
+    _qw: QuantizedWeight
+
+    @staticmethod
+    def __new__(cls, qw: QuantizedWeight):
+        t = torch.Tensor._make_wrapper_subclass(
+            cls, tuple(qw.q.shape), dtype=qw.dtype, device=qw.q.device, requires_grad=False
+        )
+        t._qw = qw
+        return t
+
+    def __repr__(self, *, tensor_contents=None):
+        return f"W8A16Weight(shape={tuple(self.shape)}, dtype={self.dtype}, device={self.device})"
+
+    def dense(self) -> torch.Tensor:
+        return self._qw.dense()
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func is F.linear:
+            x = args[0] if args else kwargs.get("input")
+            w = args[1] if len(args) > 1 else kwargs.get("weight")
+            b = args[2] if len(args) > 2 else kwargs.get("bias")
+            # metadata is read from the plain QuantizedWeight: a property of the
+            # subclass itself would re-enter this handler
+            if (type(w) is W8A16Weight and type(x) is torch.Tensor
+                    and (b is None or type(b) is torch.Tensor)
+                    and w._qw.dtype == torch.bfloat16 and x.dtype == torch.bfloat16
+                    and x.device == w._qw.q.device):
+                return w._qw.linear(x, b)
+        # everything else keeps torch's own behaviour: metadata reads use the
+        # wrapper's shape/dtype/device, and compute reaches __torch_dispatch__,
+        # which hands the op the dense weight
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        args, kwargs = _densify((args, kwargs or {}))
+        return func(*args, **kwargs)
+
+
+def _densify(obj):
+    if isinstance(obj, W8A16Weight):
+        return obj._qw.dense()
+    if isinstance(obj, tuple):
+        return tuple(_densify(o) for o in obj)
+    if isinstance(obj, list):
+        return [_densify(o) for o in obj]
+    if isinstance(obj, dict):
+        return {k: _densify(v) for k, v in obj.items()}
+    return obj

@@ -1,0 +1,95 @@
+"""Routing logic of ``QuantizedWeight.get()``'s tensor view, on the CPU.
+
+``F.linear(x_bf16, w.get(), b)`` (engine/model.py:168-190 through _resolve,
+engine/model.py:25-26) must reach the fused linear entry point; metadata reads
+must not materialise anything; every other op must see the dense weight.
+The kernels are stubbed here: this checks host dispatch only.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import quantization_oracle as O
+from pageserve_amd.quantization import W8A16Weight
+
+
+class FakeQW:
+    """Stands in for a GPU QuantizedWeight: records calls, no kernels."""
+
+    def __init__(self, dtype=torch.bfloat16):
+        self.q = torch.randint(-127, 128, (6, 16), dtype=torch.int8)
+        self.scale = torch.rand(6, 1) * 0.01
+        self.dtype = dtype
+        self.calls = []
+
+    def dense(self):
+        self.calls.append("dense")
+        return (self.q.float() * self.scale).to(self.dtype)
+
+    def linear(self, x, bias=None):
+        self.calls.append("linear")
+        return F.linear(x, self.dense(), bias)
+
+
+def test_f_linear_reaches_the_fused_entry_point():
+    qw = FakeQW()
+    w = W8A16Weight(qw)
+    assert w.shape == (6, 16) and w.dtype == torch.bfloat16 and w.device.type == "cpu"
+    assert qw.calls == []  # metadata only
+    x = torch.randn(3, 16).to(torch.bfloat16)
+    b = torch.randn(6).to(torch.bfloat16)
+    y = F.linear(x, w, b)
+    assert qw.calls[0] == "linear"
+    assert type(y) is torch.Tensor and y.shape == (3, 6)
+    qw.calls.clear()
+    F.linear(x, w)
+    F.linear(input=x, weight=w, bias=b)
+    assert qw.calls.count("linear") == 2
+
+
+def test_other_ops_get_the_dense_weight():
+    qw = FakeQW()
+    w = W8A16Weight(qw)
+    dense = (qw.q.float() * qw.scale).to(torch.bfloat16)
+    assert torch.equal(w + 0, dense)
+    assert torch.equal(w.t().contiguous(), dense.t().contiguous())
+    assert type(w.float()) is torch.Tensor
+    assert "linear" not in qw.calls and "dense" in qw.calls
+
+
+def test_non_bf16_activations_use_the_dense_weight():
+    qw = FakeQW(dtype=torch.float32)
+    w = W8A16Weight(qw)
+    x = torch.randn(2, 16)
+    y = F.linear(x, w)
+    assert "linear" not in qw.calls
+    torch.testing.assert_close(y, x @ (qw.q.float() * qw.scale).T)
+
+
+def test_metadata_reads_do_not_materialise():
+    qw = FakeQW()
+    w = W8A16Weight(qw)
+    _ = (w.shape, w.dtype, w.device, w.dim(), w.size(0), w.ndim, w.is_cuda, w.requires_grad, repr(w))
+    assert qw.calls == []
+
+
+def test_compare_floors_bf16_outputs_at_one_ulp():
+    ref = np.array([10.0, 0.5, -3.0], dtype=np.float32)
+    # one bf16 ulp at 10.0 is 0.0625 > 2e-2*sqrt(2): allowed only for a bf16 output
+    y = ref + np.array([0.0625, 0.0, 0.0], dtype=np.float32)
+    assert not O.compare(y, ref, 2048)["ok"]
+    assert O.compare(y, ref, 2048, bf16_out=True)["ok"]
+    y2 = ref + np.array([0.13, 0.0, 0.0], dtype=np.float32)
+    assert not O.compare(y2, ref, 2048, bf16_out=True)["ok"]
+    # small values keep the specification's absolute bound
+    y3 = ref + np.array([0.0, 0.03, 0.0], dtype=np.float32)
+    assert not O.compare(y3, ref, 2048, bf16_out=True)["ok"]
+
+
+@pytest.mark.parametrize("v,ulp", [(1.0, 2 ** -7), (10.0, 2 ** -4), (0.5, 2 ** -8), (-3.0, 2 ** -6)])
+def test_bf16_ulp(v, ulp):
+    assert O.bf16_ulp(np.array([v]))[0] == ulp

@@ -1,0 +1,144 @@
+"""W8A16 linear kernels against the fp32 dequant+matmul oracle.
+
+engine/model.py:168-170 (q/k/v, with bias), :184 (o), :188-190 (gate/up/down)
+and :193 (lm_head, fp32 logits).  Tolerance from the path's specification:
+max|y - y_ref| / max|y_ref| <= 1e-2 and max|y - y_ref| <= 2e-2 * sqrt(K/1024),
+with y_ref = x . fp32(q * scale)^T (+ b) summed in float64 (oracle.linear).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import activations, bf16_gpu, report, to_np, weights
+from oracle import quantization_oracle as O
+from pageserve_amd import quantization as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(gpu, seed, m, n, k, bias=False):
+    w = weights(seed, n, k)
+    x = activations(seed + 1, m, k)
+    b = O.round_to_bf16(np.random.default_rng(seed + 2).standard_normal(n).astype(np.float32)) if bias else None
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu))
+    q, s = O.quantize_per_channel(w)
+    return qw, q, s, x, b
+
+
+# decode (skinny kernel, m <= 16) and prefill (tile kernel) shapes, including
+# ragged n (not a multiple of 16 / 128) and k not a multiple of 64
+SHAPES = [
+    (1, 2048, 2048), (1, 256, 2048), (1, 11008, 2048), (1, 2048, 11008),
+    (4, 2048, 2048), (4, 11008, 2048), (16, 2048, 11008), (16, 256, 2048),
+    (2, 100, 80), (3, 1, 16), (5, 17, 48), (7, 4864, 896), (15, 130, 1040), (1, 33, 112),
+    (17, 64, 64), (31, 300, 208), (64, 2048, 2048), (100, 1000, 336), (127, 129, 2048),
+    (128, 2048, 2048), (129, 256, 2048), (256, 11008, 2048), (512, 2048, 2048), (512, 2048, 11008),
+    (300, 2560, 2048),
+]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_matches_oracle(gpu, m, n, k):
+    qw, q, s, x, _ = _problem(gpu, 100 + m + n + k, m, n, k)
+    y = qw.linear(bf16_gpu(x, gpu))
+    assert y.dtype == torch.bfloat16 and y.shape == (m, n)
+    report(to_np(y), O.linear(x, q, s), k, f"linear m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 16, 40, 256])
+def test_linear_with_bias(gpu, m):
+    qw, q, s, x, b = _problem(gpu, 7 + m, m, 2048, 2048, bias=True)
+    y = qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu))
+    report(to_np(y), O.linear(x, q, s, b), 2048, f"linear+bias m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 8, 20, 256])
+def test_fp32_output(gpu, m):
+    qw, q, s, x, _ = _problem(gpu, 50 + m, m, 1536, 2048)
+    y = qw.linear(bf16_gpu(x, gpu), out_dtype=torch.float32)
+    assert y.dtype == torch.float32
+    r = report(to_np(y), O.linear(x, q, s), 2048, f"fp32 out m={m}", bf16_out=False)
+    # fp32 output carries no bf16 rounding: far inside the bound
+    assert r["rel"] < 1e-4
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 64, 512])
+def test_grouped_qkv_matches_separate_calls(gpu, m):
+    """q/k/v (engine/model.py:168-170) in one launch: each output equals the
+    single-weight kernel's output bit for bit, and the oracle within tolerance."""
+    k = 2048
+    x = activations(7000 + m, m, k)  # seeds distinct from the weights
+    xs = bf16_gpu(x, gpu)
+    ws, qs, ss, bs = [], [], [], []
+    for j, n in enumerate((2048, 256, 256)):
+        w = weights(901 + j, n, k)
+        ws.append(Q.QuantizedWeight(torch.from_numpy(w).to(gpu)))
+        q, s = O.quantize_per_channel(w)
+        qs.append(q)
+        ss.append(s)
+        bs.append(O.round_to_bf16(np.random.default_rng(950 + j).standard_normal(n).astype(np.float32)))
+    bt = [bf16_gpu(b, gpu) for b in bs]
+    outs = Q.linear_group(xs, ws, bt)
+    for j in range(3):
+        single = ws[j].linear(xs, bt[j])
+        assert torch.equal(outs[j], single), f"group member {j} differs from its single launch"
+        report(to_np(outs[j]), O.linear(x, qs[j], ss[j], bs[j]), k, f"qkv[{j}] m={m}")
+
+
+def test_leading_dims_and_noncontiguous_input(gpu):
+    qw, q, s, x, _ = _problem(gpu, 3, 6, 512, 256)
+    xt = bf16_gpu(x, gpu).reshape(2, 3, 256)
+    y = qw.linear(xt)
+    assert y.shape == (2, 3, 512)
+    report(to_np(y.reshape(6, 512)), O.linear(x, q, s), 256, "3-D input")
+    # a transposed view: the wrapper copies it to a contiguous buffer
+    xT = bf16_gpu(np.ascontiguousarray(x.T), gpu).t()
+    report(to_np(qw.linear(xT)), O.linear(x, q, s), 256, "non-contiguous input")
+
+
+def test_full_size_prefill_sampled(gpu):
+    """m = 2048 (the largest prefill chunk) on gate_proj's shape: every output
+    row and column block checked on a random sample against the oracle."""
+    m, n, k = 2048, 11008, 2048
+    qw, q, s, x, _ = _problem(gpu, 4242, m, n, k)
+    y = to_np(qw.linear(bf16_gpu(x, gpu)))
+    rng = np.random.default_rng(1)
+    rows = rng.choice(m, 96, replace=False)
+    cols = rng.choice(n, 512, replace=False)
+    ref = O.linear(x[rows], q[cols], s[cols])
+    report(y[np.ix_(rows, cols)], ref, k, "m=2048 sample")
+    assert np.isfinite(y).all()
+
+
+def test_deterministic(gpu):
+    qw, q, s, x, _ = _problem(gpu, 77, 512, 2048, 11008)
+    xs = bf16_gpu(x, gpu)
+    a = qw.linear(xs)
+    b = qw.linear(xs)
+    assert torch.equal(a, b)
+    qw1, *_ = _problem(gpu, 78, 1, 2048, 11008)
+    xs1 = bf16_gpu(activations(5, 1, 11008), gpu)
+    assert torch.equal(qw1.linear(xs1), qw1.linear(xs1))
+
+
+def test_empty_inputs(gpu):
+    qw, *_ = _problem(gpu, 1, 4, 64, 64)
+    y = qw.linear(torch.zeros((0, 64), dtype=torch.bfloat16, device=gpu))
+    assert y.shape == (0, 64)
+
+
+def test_bad_inputs_raise(gpu):
+    qw, *_ = _problem(gpu, 1, 4, 64, 64)
+    with pytest.raises(TypeError, match="bf16"):
+        qw.linear(torch.zeros((2, 64), dtype=torch.float32, device=gpu))
+    with pytest.raises(ValueError, match="features"):
+        qw.linear(torch.zeros((2, 32), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError, match="bias"):
+        qw.linear(torch.zeros((2, 64), dtype=torch.bfloat16, device=gpu), torch.zeros(3, dtype=torch.bfloat16,
+                                                                                      device=gpu))
+    odd = Q.QuantizedWeight(torch.randn(8, 40, device=gpu))
+    with pytest.raises(ValueError, match="multiple of 16"):
+        odd.linear(torch.zeros((2, 40), dtype=torch.bfloat16, device=gpu))

@@ -1,0 +1,150 @@
+"""Quantizer and dequantizer kernels against the oracle: bit-exact.
+
+engine/quantization.py:16-27.  q and scale must equal the oracle bit for bit
+(integer and exactly specified fp32 arithmetic); dequantize likewise.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import weights
+from oracle import quantization_oracle as O
+from pageserve_amd import quantization as Q
+from test_oracle_pins import adversarial_rows, kat_rows, random_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_quant(w_np: np.ndarray, device, dtype=torch.float32):
+    w = torch.from_numpy(w_np).to(device)
+    if dtype == torch.bfloat16:
+        w = torch.from_numpy(O.f32_to_bf16_bits(w_np).view(np.int16).copy()).view(torch.bfloat16).to(device)
+    q, s = Q.quantize_per_channel(w)
+    torch.cuda.synchronize()
+    return q.cpu().numpy(), s.cpu().numpy()
+
+
+def _assert_bit_exact(q, s, q_ref, s_ref, what):
+    assert q.dtype == np.int8 and s.dtype == np.float32 and s.shape == s_ref.shape, what
+    bad = np.flatnonzero(s.view(np.uint32).ravel() != s_ref.view(np.uint32).ravel())
+    assert bad.size == 0, f"{what}: {bad.size} scales differ, first row {bad[:5]}"
+    diff = np.argwhere(q != q_ref)
+    assert diff.size == 0, f"{what}: {len(diff)} q values differ, first {diff[:5].tolist()}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_known_answer_rows(gpu, dtype):
+    w, q_exp, s_exp = kat_rows()
+    q, s = _gpu_quant(w, gpu, dtype)
+    _assert_bit_exact(q, s, q_exp, s_exp, f"KAT {dtype}")
+
+
+def test_adversarial_rows(gpu):
+    w = adversarial_rows(rows=64, per_row=64)
+    q, s = _gpu_quant(w, gpu)
+    q_ref, s_ref = O.quantize_per_channel(w)
+    _assert_bit_exact(q, s, q_ref, s_ref, "adversarial")
+
+
+@pytest.mark.parametrize(
+    "n,k",
+    [(1, 1), (3, 7), (17, 100), (8, 40), (64, 128), (4864, 896), (256, 2048), (2048, 11008), (300, 4100)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_random_shapes_bit_exact(gpu, n, k, dtype):
+    w = random_matrix(1000 + n + k, n, k) if n >= 4 else weights(7, n, k)
+    if dtype == torch.bfloat16:
+        w = O.round_to_bf16(w)
+    q, s = _gpu_quant(w, gpu, dtype)
+    if dtype == torch.bfloat16:
+        q_ref, s_ref = O.quantize_per_channel(O.f32_to_bf16_bits(w), bf16_bits=True)
+    else:
+        q_ref, s_ref = O.quantize_per_channel(w)
+    _assert_bit_exact(q, s, q_ref, s_ref, f"[{n},{k}] {dtype}")
+
+
+def test_misaligned_view_takes_the_scalar_path(gpu):
+    base = weights(5, 33 * 65 + 1, 1).reshape(-1)
+    w_np = base[1:].reshape(33, 65)
+    wt = torch.from_numpy(base).to(gpu)[1:].view(33, 65)  # data pointer off by 4 bytes
+    q, s = Q.quantize_per_channel(wt)
+    q_ref, s_ref = O.quantize_per_channel(w_np)
+    _assert_bit_exact(q.cpu().numpy(), s.cpu().numpy(), q_ref, s_ref, "misaligned")
+
+
+def test_cpu_weight_round_trips_through_the_gpu(gpu):
+    w = weights(8, 96, 256)
+    q, s = Q.quantize_per_channel(torch.from_numpy(w))
+    assert q.device.type == "cpu" and s.device.type == "cpu"
+    q_ref, s_ref = O.quantize_per_channel(w)
+    _assert_bit_exact(q.numpy(), s.numpy(), q_ref, s_ref, "cpu-resident weight")
+
+
+def test_lm_head_shape_full_size(gpu):
+    """[151936, 2048] (the Qwen2.5 vocabulary): bit-exact on a row sample,
+    and exact invariants on every row."""
+    n, k = 151936, 2048
+    gen = torch.Generator(device=gpu).manual_seed(1234)
+    w = torch.randn((n, k), generator=gen, device=gpu, dtype=torch.float32) * 0.02
+    q, s = Q.quantize_per_channel(w)
+    # every nonzero row's absmax element maps to exactly +-127; |q| <= 127
+    qmax = q.abs().amax(dim=1)
+    assert int(qmax.min()) == 127 and int(qmax.max()) == 127
+    assert int(q.min()) >= -127
+    # scale == max(absmax, 1e-8) / 127 with an IEEE fp32 divide (numpy on the
+    # host; torch's GPU division by a scalar multiplies by a reciprocal)
+    absmax = w.abs().amax(dim=1, keepdim=True).cpu().numpy()
+    s_all = (np.maximum(absmax, np.float32(1e-8)) / np.float32(127.0)).astype(np.float32)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_all.view(np.uint32))
+    rows = np.concatenate([np.arange(0, 4096), np.random.default_rng(0).choice(n, 4096, replace=False),
+                           np.arange(n - 64, n)])
+    w_rows = w[torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    q_ref, s_ref = O.quantize_per_channel(w_rows)
+    _assert_bit_exact(q[torch.from_numpy(rows).to(gpu)].cpu().numpy(),
+                      s[torch.from_numpy(rows).to(gpu)].cpu().numpy(), q_ref, s_ref, "lm_head rows")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+@pytest.mark.parametrize("n,k", [(64, 128), (5, 7), (2048, 2048)])
+def test_dequantize_bit_exact(gpu, dtype, n, k):
+    w = random_matrix(77 + k, n, k)
+    q_ref, s_ref = O.quantize_per_channel(w)
+    qt = torch.from_numpy(q_ref).to(gpu)
+    st = torch.from_numpy(s_ref).to(gpu)
+    out = Q.dequantize(qt, st, dtype)
+    assert out.dtype == dtype and out.shape == (n, k) and out.device == qt.device
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16", torch.float64: "f32"}[dtype]
+    ref = O.dequantize(q_ref, s_ref, name)
+    got = out.cpu()
+    if dtype == torch.bfloat16:
+        np.testing.assert_array_equal(got.view(torch.int16).numpy().view(np.uint16), ref)
+    elif dtype == torch.float64:
+        np.testing.assert_array_equal(got.numpy(), ref.astype(np.float64))
+    else:
+        np.testing.assert_array_equal(got.numpy().view(np.uint8), ref.view(np.uint8))
+
+
+def test_quantized_weight_matches_reference_contract(gpu):
+    """tests/test_quantization.py:14-46 run on the GPU path."""
+    torch.manual_seed(0)
+    w = torch.randn(64, 128, dtype=torch.float32)
+    qw = Q.QuantizedWeight(w.to(gpu))
+    assert qw.q.dtype == torch.int8 and qw.scale.shape == (64, 1) and qw.dtype == torch.float32
+    rec = qw.get()
+    err = (w - rec.cpu()).abs().max().item()
+    step = (w.abs().amax(dim=1, keepdim=True) / 127.0).max().item()
+    assert err <= step
+    big = Q.QuantizedWeight(torch.randn(2048, 2048).to(gpu))
+    assert big.storage_bytes < 2048 * 2048 * 4 / 3
+    torch.manual_seed(1)
+    x = torch.randn(8, 128)
+    wt = torch.randn(64, 128)
+    qw = Q.QuantizedWeight(wt.to(gpu))
+    exp = x @ wt.T
+    act = x @ qw.get().cpu().T
+    assert (exp - act).abs().max().item() / exp.abs().max().item() < 0.05
+    # .to() moves in place and returns self (engine/quantization.py:43-46)
+    assert qw.to("cpu") is qw and qw.q.device.type == "cpu"

@@ -1,0 +1,61 @@
+"""Fused SwiGLU (engine/model.py:188-190) against the oracle.
+
+act = silu(x Wg^T) * (x Wu^T) computed in fp32 and rounded once to bf16;
+out = act Wd^T.  The oracle keeps everything in fp32/float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import activations, bf16_gpu, report, to_np, weights
+from oracle import quantization_oracle as O
+from pageserve_amd import quantization as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _mlp_weights(gpu, seed, inter, hidden):
+    ws = {}
+    for j, (name, shape) in enumerate((("gate", (inter, hidden)), ("up", (inter, hidden)),
+                                       ("down", (hidden, inter)))):
+        w = weights(seed + j, *shape)
+        ws[name] = (Q.QuantizedWeight(torch.from_numpy(w).to(gpu)), *O.quantize_per_channel(w))
+    return ws
+
+
+@pytest.mark.parametrize("m,inter,hidden", [(1, 11008, 2048), (4, 11008, 2048), (16, 11008, 2048),
+                                            (17, 11008, 2048), (128, 11008, 2048), (512, 11008, 2048),
+                                            (3, 100, 48), (40, 300, 208)])
+def test_swiglu_matches_oracle(gpu, m, inter, hidden):
+    ws = _mlp_weights(gpu, 10 + m + inter, inter, hidden)
+    x = activations(m, m, hidden)
+    act = Q.swiglu(bf16_gpu(x, gpu), ws["gate"][0], ws["up"][0])
+    assert act.dtype == torch.bfloat16 and act.shape == (m, inter)
+    ref = O.swiglu(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2])
+    report(to_np(act), ref, hidden, f"swiglu m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 512])
+def test_mlp_config(gpu, m):
+    """The fused SwiGLU MLP workload: x [m, 2048], gate/up [11008, 2048],
+    down [2048, 11008]; out = down(silu(gate(x)) * up(x))."""
+    ws = _mlp_weights(gpu, 4000, 11008, 2048)
+    x = activations(4100 + m, m, 2048)
+    out = Q.mlp(bf16_gpu(x, gpu), ws["gate"][0], ws["up"][0], ws["down"][0])
+    ref = O.mlp(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2], ws["down"][1], ws["down"][2])
+    report(to_np(out), ref, 11008, f"mlp m={m}")
+
+
+def test_swiglu_equals_unfused_composition(gpu):
+    """Same as gate and up as separate fp32-output linears, combined in fp32."""
+    ws = _mlp_weights(gpu, 77, 1024, 512)
+    x = bf16_gpu(activations(3, 8, 512), gpu)
+    g = ws["gate"][0].linear(x, out_dtype=torch.float32)
+    u = ws["up"][0].linear(x, out_dtype=torch.float32)
+    expect = (torch.nn.functional.silu(g) * u).to(torch.bfloat16).float()
+    got = Q.swiglu(x, ws["gate"][0], ws["up"][0]).float()
+    # same fp32 accumulations; silu rounding may differ by one bf16 ulp
+    assert ((got - expect).abs() <= expect.abs() * 2 ** -7 + 1e-6).all()

@@ -1,0 +1,72 @@
+"""The C-ABI library: loads, exports exactly what include/pageserve_amd.h
+declares, and rejects bad arguments before touching a GPU (CPU-only)."""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import pytest
+
+from pageserve_amd import _native
+
+
+def test_header_declares_the_bound_symbols():
+    assert sorted(_native.SIGNATURES) == _native.header_symbols()
+
+
+def test_library_exports_every_header_symbol(native_lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    for name in _native.header_symbols():
+        assert name in exported, f"{name} declared in the header but not exported"
+        assert hasattr(native_lib, name)
+
+
+def test_abi_version_and_error_strings(native_lib):
+    assert native_lib.pgs_abi_version() == _native.ABI_VERSION
+    assert native_lib.pgs_error_string(0) == b"ok"
+    for code in (1, 2, 3, 4):
+        assert native_lib.pgs_error_string(code) not in (b"ok", b"unknown error")
+    assert native_lib.pgs_error_string(99) == b"unknown error"
+
+
+@pytest.mark.parametrize(
+    "call, needle",
+    [
+        (lambda L: L.pgs_quantize_per_channel(None, 0, -1, 4, None, None, None), b"negative size"),
+        (lambda L: L.pgs_quantize_per_channel(None, 7, 4, 4, None, None, None), b"dtype"),
+        (lambda L: L.pgs_quantize_per_channel(None, 0, 4, 4, None, None, None), b"null pointer"),
+        (lambda L: L.pgs_dequantize(None, None, 2, -3, None, 0, None), b"negative size"),
+        (lambda L: L.pgs_dequantize(ctypes.c_void_p(16), ctypes.c_void_p(16), 2, 16, ctypes.c_void_p(16), 9, None),
+         b"dtype"),
+        (lambda L: L.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None), b"multiple of 16"),
+        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(8), None, None, None, None, 1, 1, 4, 16, None), b"aligned"),
+        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(16), None, None, None, None, 5, 1, 4, 16, None), b"dtype"),
+        (lambda L: L.pgs_w8a16_linear_group(ctypes.c_void_p(16), None, 0, 1, 1, 16, None), b"n_outs"),
+        (lambda L: L.pgs_w8a16_swiglu(None, None, None, None, None, None, -1, 4, 16, None), b"negative size"),
+    ],
+)
+def test_bad_arguments_are_rejected_without_launching(native_lib, call, needle):
+    rc = call(native_lib)
+    assert rc in (1, 2)
+    assert needle in native_lib.pgs_last_error()
+
+
+def test_empty_problems_are_no_ops(native_lib):
+    # m == 0 or n == 0: nothing to compute, success, nothing launched
+    assert native_lib.pgs_w8a16_linear(ctypes.c_void_p(256), None, None, None, None, 1, 0, 8, 64, None) == 0
+    assert native_lib.pgs_quantize_per_channel(None, 0, 0, 64, None, None, None) == 0
+    assert native_lib.pgs_dequantize(None, None, 0, 64, None, 0, None) == 0
+
+
+def test_check_raises_with_library_message(native_lib):
+    rc = native_lib.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        _native.check(rc, "w8a16 linear")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_native.NativeLibraryError, match="not found"):
+        _native.load(tmp_path / "nope.so")
