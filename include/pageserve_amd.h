@@ -6,17 +6,36 @@
  * are asynchronous on that stream; no entry point synchronises the host and
  * none allocates device memory.  Buffers are owned by the caller.
  *
+ * Workspace (linear entry points): some shapes split the reduction over K
+ * across workgroups and combine the partial tiles through a caller-provided
+ * device buffer.  pgs_w8a16_workspace_bytes() gives the size a call needs
+ * (0 = none).  The buffer must be 256-byte aligned; its contents on entry do
+ * not matter.  Calls that share a workspace must be ordered (same stream, or
+ * synchronised); overlapping calls on one workspace race.  Passing NULL
+ * disables the split (always correct, slower for short-N shapes).
+ *
  * Return value: PGS_OK (0) or one of the PGS_ERR_* codes below.  A call that
  * returns an error has launched nothing.  pgs_last_error() gives a
  * human-readable message for the calling thread's most recent failure.
  *
- * Layouts (row-major, densely packed, no leading-dimension argument):
- *   weight w   [n, k]  fp32 or bf16   (out_features, in_features)
- *   q          [n, k]  int8           per-output-row symmetric quantization
+ * Layouts (no leading-dimension argument):
+ *   weight w   [n, k]  fp32 or bf16   row-major (out_features, in_features)
+ *   q          [n, k]  int8           row-major, per-output-row symmetric
+ *                                     quantization (QuantizedWeight.q)
+ *   qp         packed  int8           the same values in "MFMA tile" order,
+ *                                     pgs_packed_bytes(n, k) bytes: 16-row x
+ *                                     64-column blocks of 1 KiB, stored
+ *                                     [ceil(n/16)][ceil(k/64)]; inside a block
+ *                                     byte 16*l + b (l = 0..63, b = 0..15) is
+ *                                     q[16*blk_row + l%16][64*blk_col +
+ *                                     16*(l/16) + b]; padding is zero.  The
+ *                                     linear entry points read weights only in
+ *                                     this layout (one contiguous KiB per
+ *                                     wavefront load).
  *   scale      [n]     fp32           (the reference stores it as [n, 1])
- *   x          [m, k]  bf16           activations
+ *   x          [m, k]  bf16           row-major activations
  *   bias       [n]     bf16           optional (NULL = none)
- *   y          [m, n]  bf16 or fp32   y = x . (q * scale)^T + bias
+ *   y          [m, n]  bf16 or fp32   row-major, y = x . (q * scale)^T + bias
  *
  * Reference interface (Rakshit-gen/pageserve, a Python package with no FFI):
  * each entry point below names the Python function or call site it replaces.
@@ -65,6 +84,29 @@ int pgs_quantize_per_channel(const void* w, int w_dtype, int64_t n, int64_t k,
                              int8_t* q, float* scale, void* stream);
 
 /*
+ * quantize_per_channel with the int8 result written in the packed layout
+ * (same values as pgs_quantize_per_channel; padding zeroed).  This is how
+ * QuantizedWeight(weight) stores its weight (engine/quantization.py:36-38).
+ */
+int pgs_quantize_per_channel_packed(const void* w, int w_dtype, int64_t n,
+                                    int64_t k, int8_t* qp, float* scale,
+                                    void* stream);
+
+/* Bytes of the packed layout of an [n, k] int8 matrix (-1 for bad sizes). */
+int64_t pgs_packed_bytes(int64_t n, int64_t k);
+
+/*
+ * Row-major q -> packed qp (padding written as zero), and back.  No
+ * counterpart in the reference, which only has the row-major form
+ * (QuantizedWeight.q, engine/quantization.py:38): unpack is how that form
+ * is produced from the packed storage.
+ */
+int pgs_pack_weight(const int8_t* q, int64_t n, int64_t k, int8_t* qp,
+                    void* stream);
+int pgs_unpack_weight(const int8_t* qp, int64_t n, int64_t k, int8_t* q,
+                      void* stream);
+
+/*
  * Replaces dequantize(q, scale, dtype) -- engine/quantization.py:26-27.
  *   out[r,j] = dtype(float(q[r,j]) * scale[r])  (fp32 product, then one
  *   round-to-nearest-even conversion to out_dtype).  Bit-exact.
@@ -73,27 +115,32 @@ int pgs_quantize_per_channel(const void* w, int w_dtype, int64_t n, int64_t k,
 int pgs_dequantize(const int8_t* q, const float* scale, int64_t n, int64_t k,
                    void* out, int out_dtype, void* stream);
 
+/* dequantize from the packed layout; row-major [n, k] output, bit-exact. */
+int pgs_dequantize_packed(const int8_t* qp, const float* scale, int64_t n,
+                          int64_t k, void* out, int out_dtype, void* stream);
+
 /*
  * Replaces F.linear(x, _resolve(W), b) for a QuantizedWeight W --
  * engine/model.py:25-26 (_resolve -> QuantizedWeight.get -> dequantize) feeding
  * the projections at engine/model.py:168-170 (q/k/v, with bias), :184 (o),
  * :188-190 (gate, up, down) and, with y_dtype = PGS_DTYPE_F32, the lm_head
  * at engine/model.py:193.
- *   y[i,r] = sum_j x[i,j] * q[r,j] * scale[r] (+ bias[r]),  fp32 accumulate.
- * The dense weight is never materialised.  y_dtype: PGS_DTYPE_BF16 or
+ *   y[i,r] = sum_j x[i,j] * q[r,j] * scale[r] (+ bias[r]),  fp32 accumulate,
+ * with the weight given packed (qp).  The dense weight is never materialised.  y_dtype: PGS_DTYPE_BF16 or
  * PGS_DTYPE_F32.  Dispatches on m: the skinny kernel for m <= 16, the
  * MFMA tile kernel above.
  */
-int pgs_w8a16_linear(const void* x, const int8_t* q, const float* scale,
+int pgs_w8a16_linear(const void* x, const int8_t* qp, const float* scale,
                      const void* bias, void* y, int y_dtype, int64_t m,
-                     int64_t n, int64_t k, void* stream);
+                     int64_t n, int64_t k, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /*
  * One output of a grouped linear: several quantized weights that read the
  * same activations (the q/k/v triple of engine/model.py:168-170).
  */
 typedef struct pgs_linear_out {
-  const int8_t* q;     /* [n, k] int8 */
+  const int8_t* qp;    /* [n, k] int8, packed layout */
   const float* scale;  /* [n] fp32 */
   const void* bias;    /* [n] bf16 or NULL */
   void* y;             /* [m, n] of y_dtype */
@@ -110,6 +157,7 @@ typedef struct pgs_linear_out {
  */
 int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
                            int n_outs, int y_dtype, int64_t m, int64_t k,
+                           void* workspace, size_t workspace_bytes,
                            void* stream);
 
 /*
@@ -117,12 +165,24 @@ int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
  * -- engine/model.py:188-190 -- with one fused launch:
  *   act[i,r] = silu(g) * u,  g = sum_j x[i,j] q_gate[r,j] * s_gate[r],
  *                            u = sum_j x[i,j] q_up[r,j] * s_up[r]
+ * (both weights packed)
  * computed in fp32 and rounded once to bf16.  act: bf16 [m, n].
  * The down projection is a separate pgs_w8a16_linear call on act.
  */
-int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float* s_gate,
-                     const int8_t* q_up, const float* s_up, void* act,
-                     int64_t m, int64_t n, int64_t k, void* stream);
+int pgs_w8a16_swiglu(const void* x, const int8_t* qp_gate, const float* s_gate,
+                     const int8_t* qp_up, const float* s_up, void* act,
+                     int64_t m, int64_t n, int64_t k, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes a linear call needs (0 = none): n[0..n_outs-1] are the
+ * out_features of its members (one member for pgs_w8a16_linear; for
+ * pgs_w8a16_swiglu pass swiglu = 1 and n[0] = intermediate size).  The value
+ * is exact for the same (m, n, k) and never larger than the plan needs.
+ * No counterpart in the reference, whose dense F.linear needs no workspace.
+ */
+size_t pgs_w8a16_workspace_bytes(int64_t m, const int64_t* n, int n_outs,
+                                 int64_t k, int swiglu);
 
 #ifdef __cplusplus
 }

@@ -113,6 +113,31 @@ def dequantize(q: np.ndarray, scale: np.ndarray, dtype: str = "f32") -> np.ndarr
 
 
 # --------------------------------------------------------------------------
+# packed tile layout of the int8 weight (this build's storage format; no
+# counterpart in the reference, whose q is row-major)
+# --------------------------------------------------------------------------
+
+def pack_tiles(q: np.ndarray) -> np.ndarray:
+    """Row-major int8 [N,K] -> flat packed bytes: 16-row x 64-column blocks of
+    1 KiB in [ceil(N/16)][ceil(K/64)] order; inside a block byte 16*l + b is
+    q[16*tr + l%16, 64*tc + 16*(l//16) + b]; padding zero."""
+    q = np.asarray(q, dtype=np.int8)
+    n, k = q.shape
+    tn, tk = -(-n // 16), -(-k // 64)
+    padded = np.zeros((tn * 16, tk * 64), dtype=np.int8)
+    padded[:n, :k] = q
+    # [tn, 16 rows, tk, 4 groups, 16 bytes] -> [tn, tk, group, row, byte]
+    blocks = padded.reshape(tn, 16, tk, 4, 16).transpose(0, 2, 3, 1, 4)
+    return np.ascontiguousarray(blocks).reshape(-1)
+
+
+def unpack_tiles(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    tn, tk = -(-n // 16), -(-k // 64)
+    blocks = np.asarray(packed, dtype=np.int8).reshape(tn, tk, 4, 16, 16).transpose(0, 3, 1, 2, 4)
+    return np.ascontiguousarray(blocks).reshape(tn * 16, tk * 64)[:n, :k]
+
+
+# --------------------------------------------------------------------------
 # a5-a8: the fp32 dequant-and-matmul (engine/model.py:168-170,184,188-190,193)
 # --------------------------------------------------------------------------
 

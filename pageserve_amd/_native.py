@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 
 class NativeLibraryError(RuntimeError):
@@ -34,7 +34,7 @@ class LinearOut(ctypes.Structure):
     """``pgs_linear_out`` of include/pageserve_amd.h."""
 
     _fields_ = [
-        ("q", ctypes.c_void_p),
+        ("qp", ctypes.c_void_p),
         ("scale", ctypes.c_void_p),
         ("bias", ctypes.c_void_p),
         ("y", ctypes.c_void_p),
@@ -45,6 +45,7 @@ class LinearOut(ctypes.Structure):
 _VP = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
+_SZ = ctypes.c_size_t
 
 # name -> (restype, argtypes); every symbol the header declares
 SIGNATURES = {
@@ -53,9 +54,15 @@ SIGNATURES = {
     "pgs_last_error": (ctypes.c_char_p, []),
     "pgs_quantize_per_channel": (_INT, [_VP, _INT, _I64, _I64, _VP, _VP, _VP]),
     "pgs_dequantize": (_INT, [_VP, _VP, _I64, _I64, _VP, _INT, _VP]),
-    "pgs_w8a16_linear": (_INT, [_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP]),
-    "pgs_w8a16_linear_group": (_INT, [_VP, ctypes.POINTER(LinearOut), _INT, _INT, _I64, _I64, _VP]),
-    "pgs_w8a16_swiglu": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP]),
+    "pgs_quantize_per_channel_packed": (_INT, [_VP, _INT, _I64, _I64, _VP, _VP, _VP]),
+    "pgs_packed_bytes": (_I64, [_I64, _I64]),
+    "pgs_pack_weight": (_INT, [_VP, _I64, _I64, _VP, _VP]),
+    "pgs_unpack_weight": (_INT, [_VP, _I64, _I64, _VP, _VP]),
+    "pgs_dequantize_packed": (_INT, [_VP, _VP, _I64, _I64, _VP, _INT, _VP]),
+    "pgs_w8a16_linear": (_INT, [_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_linear_group": (_INT, [_VP, ctypes.POINTER(LinearOut), _INT, _INT, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_swiglu": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
 }
 
 _lock = threading.Lock()

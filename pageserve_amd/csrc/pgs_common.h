@@ -61,11 +61,32 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------
+// packed weight layout
+// ---------------------------------------------------------------------------
+//
+// The linear kernels read int8 weights in "MFMA tile" order: the [n, k]
+// matrix is cut into 16-row x 64-k blocks, stored block-row by block-row
+// ([ceil(n/16)][ceil(k/64)] blocks of 1 KiB), and inside a block the 16 bytes
+// of lane l (0..63) are row l%16, columns 16*(l/16) .. +15.  One 128-bit load
+// per lane then fetches a whole contiguous KiB that is exactly the A operand
+// of two v_mfma_f32_16x16x32_bf16.  Padding rows/columns are zero.
+
+__host__ __device__ inline int64_t packed_kblocks(int64_t k) { return (k + 63) / 64; }
+__host__ __device__ inline int64_t packed_bytes(int64_t n, int64_t k) {
+  return ((n + 15) / 16) * packed_kblocks(k) * 1024;
+}
+// byte offset of element (r, j) of an [n, k] matrix with kb = packed_kblocks(k)
+__host__ __device__ inline int64_t packed_offset(int64_t r, int64_t j, int64_t kb) {
+  return ((r >> 4) * kb + (j >> 6)) * 1024 + (((r & 15) + 16 * ((j & 63) >> 4)) << 4) + (j & 15);
+}
+
+// ---------------------------------------------------------------------------
 // host-side error handling (defined in pgs_api.hip)
 // ---------------------------------------------------------------------------
 
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+int fill_zero(void* p, int64_t bytes, hipStream_t st);  // kernel fill (no memset node in captured graphs)
 
 inline bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;

@@ -1,0 +1,95 @@
+// Shared definitions of the W8A16 linear kernels (skinny and tile GEMM).
+//
+// Operand convention of every kernel: v_mfma_f32_16x16x32_bf16 with the
+// weight as A (16 weight rows) and the activations as B (16 tokens).  Lane l
+// supplies A row l%16 and B column l%16, both over the same 8 consecutive k
+// values 8*(l/16)..+7 of a 32-k step, so a 16-byte load of 16 int8 weights
+// feeds two MFMAs.  The accumulator lane l holds D[4*(l/16)+r][l%16], r=0..3.
+#pragma once
+
+#include "pgs_common.h"
+
+namespace pgs {
+
+// Members of one launch that share the activations x (q/k/v), or the SwiGLU
+// pair (member 0 = gate, member 1 = up, output in member 0's y).
+struct GroupArgs {
+  const int8_t* q[PGS_MAX_GROUP];
+  const float* scale[PGS_MAX_GROUP];
+  const uint16_t* bias[PGS_MAX_GROUP];
+  void* y[PGS_MAX_GROUP];
+  int32_t n[PGS_MAX_GROUP];
+  int32_t unit_begin[PGS_MAX_GROUP + 1];  // first work unit (tile) of each member
+  int32_t n_outs;
+};
+
+struct Problem {
+  const uint16_t* x;
+  GroupArgs args;
+  int m, k;
+  int nmat;  // 1 = linear / group, 2 = SwiGLU pair
+  bool out_f32;
+  float* partials;  // split-K workspace (null: no split)
+  size_t partial_bytes;
+};
+
+// Launch plan of the skinny kernel (m <= 16).
+struct SkinnyPlan {
+  int tiles;   // 16-row tiles over all members
+  int nw;      // waves per workgroup (split the workgroup's K range)
+  int splits;  // workgroups per tile (split K across workgroups)
+};
+
+// Launch plan of the tile GEMM (m > 16).
+struct GemmPlan {
+  int bm, bn;     // output tile (tokens x weight rows)
+  int tiles_m, tiles_n, tiles;
+  int splits;     // workgroups per output tile along K
+};
+
+SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split);
+size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat);
+int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st);
+
+GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split);
+size_t gemm_partial_bytes(const GemmPlan& p, int nmat);
+int launch_gemm(Problem& p, const GemmPlan& plan, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+// Selects member [g] with constant indices only (a dynamic index into a
+// kernel-argument array would spill the struct to scratch).
+template <typename T, int L>
+__device__ __forceinline__ T pick(const T (&arr)[L], int g) {
+  T v = arr[0];
+#pragma unroll
+  for (int i = 1; i < L; ++i) v = (g == i) ? arr[i] : v;
+  return v;
+}
+
+__device__ __forceinline__ int member_of(const GroupArgs& a, int unit) {
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (i < a.n_outs && unit >= a.unit_begin[i]) ? i : g;
+  return g;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Streaming load: the weights are read once per call, so keep them from
+// displacing reusable lines (activations, partials) in the caches.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+template <bool OUT_F32>
+__device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
+  if constexpr (OUT_F32)
+    reinterpret_cast<float*>(y)[idx] = v;
+  else
+    reinterpret_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(v);
+}
+
+}  // namespace pgs

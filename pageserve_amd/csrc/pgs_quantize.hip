@@ -52,9 +52,11 @@ __device__ __forceinline__ uint32_t quantize_one(float w, float s) {
   return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(r))));
 }
 
-template <bool BF16, int VEC>
+// PACKED: write q in the packed tile layout (kb = packed_kblocks(k)) instead
+// of row-major; a VEC-element group never straddles a 16-byte lane segment.
+template <bool BF16, int VEC, bool PACKED>
 __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
-    const void* __restrict__ w, int64_t k, int8_t* __restrict__ q, float* __restrict__ scale) {
+    const void* __restrict__ w, int64_t k, int64_t kb, int8_t* __restrict__ q, float* __restrict__ scale) {
   const int64_t row = blockIdx.x;
   const int64_t nvec = k / VEC;
   const int64_t base = row * k;
@@ -81,20 +83,24 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
   for (int64_t v = threadIdx.x; v < nvec; v += kQuantThreads) {
     float f[VEC];
     load_row_vec<BF16, VEC>(w, base + v * VEC, f);
+    const int64_t dst = PACKED ? packed_offset(row, v * VEC, kb) : base + v * VEC;
     if constexpr (VEC == 8) {
       u32x2 out;
       out[0] = quantize_one(f[0], s) | (quantize_one(f[1], s) << 8) | (quantize_one(f[2], s) << 16) |
                (quantize_one(f[3], s) << 24);
       out[1] = quantize_one(f[4], s) | (quantize_one(f[5], s) << 8) | (quantize_one(f[6], s) << 16) |
                (quantize_one(f[7], s) << 24);
-      *reinterpret_cast<u32x2*>(q + base + v * VEC) = out;
+      *reinterpret_cast<u32x2*>(q + dst) = out;
     } else if constexpr (VEC == 4) {
       uint32_t out = quantize_one(f[0], s) | (quantize_one(f[1], s) << 8) | (quantize_one(f[2], s) << 16) |
                      (quantize_one(f[3], s) << 24);
-      *reinterpret_cast<uint32_t*>(q + base + v * VEC) = out;
+      *reinterpret_cast<uint32_t*>(q + dst) = out;
     } else {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) q[base + v * VEC + i] = static_cast<int8_t>(quantize_one(f[i], s));
+      for (int i = 0; i < VEC; ++i) {
+        const int64_t d = PACKED ? packed_offset(row, v * VEC + i, kb) : base + v * VEC + i;
+        q[d] = static_cast<int8_t>(quantize_one(f[i], s));
+      }
     }
   }
 }
@@ -169,6 +175,41 @@ int launch_dequant(const int8_t* q, const float* scale, int64_t n, int64_t k, vo
   return check_launch("pgs_dequantize");
 }
 
+template <bool PACKED>
+int launch_quantize(const char* fn, const void* w, int w_dtype, int64_t n, int64_t k, int8_t* q, float* scale,
+                    void* stream) {
+  if (n < 0 || k < 0)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: negative size n=%lld k=%lld", fn, (long long)n, (long long)k);
+  if (w_dtype != PGS_DTYPE_F32 && w_dtype != PGS_DTYPE_BF16)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: weight dtype code %d not fp32/bf16", fn, w_dtype);
+  if (n == 0) return PGS_OK;
+  if (n > 0x7fffffff) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: n=%lld too large", fn, (long long)n);
+  if (!scale || (k > 0 && (!w || !q))) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  const size_t esz = (w_dtype == PGS_DTYPE_F32) ? 4 : 2;
+  if (!aligned(w, esz) || !aligned(scale, 4))
+    return fail(PGS_ERR_MISALIGNED, "%s: weight/scale not aligned to element size", fn);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t kb = packed_kblocks(k);
+  if (PACKED && k > 0 && (n % 16 != 0 || k % 64 != 0)) {
+    // padding rows/columns of the packed buffer must read as zero
+    int rc = fill_zero(q, packed_bytes(n, k), st);
+    if (rc) return rc;
+  }
+  dim3 grid(static_cast<unsigned>(n)), block(kQuantThreads);
+  if (w_dtype == PGS_DTYPE_F32) {
+    if (k % 4 == 0 && aligned(w, 16) && aligned(q, 4))
+      hipLaunchKernelGGL((quantize_rows_kernel<false, 4, PACKED>), grid, block, 0, st, w, k, kb, q, scale);
+    else
+      hipLaunchKernelGGL((quantize_rows_kernel<false, 1, PACKED>), grid, block, 0, st, w, k, kb, q, scale);
+  } else {
+    if (k % 8 == 0 && aligned(w, 16) && aligned(q, 8))
+      hipLaunchKernelGGL((quantize_rows_kernel<true, 8, PACKED>), grid, block, 0, st, w, k, kb, q, scale);
+    else
+      hipLaunchKernelGGL((quantize_rows_kernel<true, 1, PACKED>), grid, block, 0, st, w, k, kb, q, scale);
+  }
+  return check_launch(fn);
+}
+
 }  // namespace
 }  // namespace pgs
 
@@ -176,31 +217,12 @@ using namespace pgs;
 
 extern "C" int pgs_quantize_per_channel(const void* w, int w_dtype, int64_t n, int64_t k, int8_t* q,
                                         float* scale, void* stream) {
-  if (n < 0 || k < 0) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_quantize_per_channel: negative size n=%lld k=%lld",
-                                  (long long)n, (long long)k);
-  if (w_dtype != PGS_DTYPE_F32 && w_dtype != PGS_DTYPE_BF16)
-    return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_quantize_per_channel: weight dtype code %d not fp32/bf16", w_dtype);
-  if (n == 0) return PGS_OK;
-  if (n > 0x7fffffff) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_quantize_per_channel: n=%lld too large", (long long)n);
-  if (!scale || (k > 0 && (!w || !q)))
-    return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_quantize_per_channel: null pointer");
-  const size_t esz = (w_dtype == PGS_DTYPE_F32) ? 4 : 2;
-  if (!aligned(w, esz) || !aligned(scale, 4))
-    return fail(PGS_ERR_MISALIGNED, "pgs_quantize_per_channel: weight/scale not aligned to element size");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid(static_cast<unsigned>(n)), block(kQuantThreads);
-  if (w_dtype == PGS_DTYPE_F32) {
-    if (k % 4 == 0 && aligned(w, 16) && aligned(q, 4))
-      hipLaunchKernelGGL((quantize_rows_kernel<false, 4>), grid, block, 0, st, w, k, q, scale);
-    else
-      hipLaunchKernelGGL((quantize_rows_kernel<false, 1>), grid, block, 0, st, w, k, q, scale);
-  } else {
-    if (k % 8 == 0 && aligned(w, 16) && aligned(q, 8))
-      hipLaunchKernelGGL((quantize_rows_kernel<true, 8>), grid, block, 0, st, w, k, q, scale);
-    else
-      hipLaunchKernelGGL((quantize_rows_kernel<true, 1>), grid, block, 0, st, w, k, q, scale);
-  }
-  return check_launch("pgs_quantize_per_channel");
+  return launch_quantize<false>("pgs_quantize_per_channel", w, w_dtype, n, k, q, scale, stream);
+}
+
+extern "C" int pgs_quantize_per_channel_packed(const void* w, int w_dtype, int64_t n, int64_t k, int8_t* packed,
+                                               float* scale, void* stream) {
+  return launch_quantize<true>("pgs_quantize_per_channel_packed", w, w_dtype, n, k, packed, scale, stream);
 }
 
 extern "C" int pgs_dequantize(const int8_t* q, const float* scale, int64_t n, int64_t k, void* out, int out_dtype,

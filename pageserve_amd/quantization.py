@@ -47,6 +47,8 @@ __all__ = [
     "linear_group",
     "swiglu",
     "mlp",
+    "pack",
+    "unpack",
 ]
 
 _DTYPE_CODE = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
@@ -101,6 +103,32 @@ def _aligned(t: torch.Tensor, n: int = 16) -> torch.Tensor:
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr() if t is not None and t.numel() else 0)
+
+
+# split-K workspaces: one per (device, stream), so that the calls sharing one
+# are ordered by their stream
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_ws_need: dict[tuple, int] = {}
+
+
+def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, swiglu: bool):
+    key = (m, ns, k, swiglu)
+    need = _ws_need.get(key)
+    if need is None:
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        need = int(lib.pgs_w8a16_workspace_bytes(m, arr, len(ns), k, int(swiglu)))
+        _ws_need[key] = need
+    if need == 0:
+        return ctypes.c_void_p(0), 0
+    wkey = (dev.index, stream)
+    ws = _workspaces.get(wkey)
+    if ws is None or ws.numel() < need:
+        size = max(need, 2 * ws.numel() if ws is not None else 0, 4 << 20)
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
+        if ws.data_ptr() % 256:
+            raise RuntimeError("pageserve_amd: workspace allocation is not 256-byte aligned")
+        _workspaces[wkey] = ws
+    return ctypes.c_void_p(ws.data_ptr()), ws.numel()
 
 
 # ---------------------------------------------------------------------------
@@ -164,6 +192,78 @@ def dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torc
 
 
 # ---------------------------------------------------------------------------
+# packed storage (the layout the linear kernels stream)
+# ---------------------------------------------------------------------------
+
+def _packed_numel(lib, n: int, k: int) -> int:
+    return int(lib.pgs_packed_bytes(n, k))
+
+
+def _quantize_packed(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """quantize_per_channel with q written in the packed layout, on the GPU."""
+    n, k = weight.shape
+    home = weight.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    w = weight if weight.dtype in (torch.float32, torch.bfloat16) else weight.float()
+    w = _aligned(w.to(dev, non_blocking=False))
+    qp = torch.empty(_packed_numel(lib, n, k), dtype=torch.int8, device=dev)
+    scale = torch.empty((n, 1), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_quantize_per_channel_packed(_ptr(w), _DTYPE_CODE[w.dtype], n, k, _ptr(qp), _ptr(scale),
+                                                 _stream(dev))
+    check(rc, "quantize_per_channel")
+    return qp, scale
+
+
+def pack(q: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 [N, K] -> the packed layout (same device as ``q``)."""
+    if q.dim() != 2 or q.dtype != torch.int8:
+        raise ValueError("q must be a 2-D int8 tensor")
+    n, k = q.shape
+    home = q.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    qd = _aligned(q.to(dev))
+    qp = torch.empty(_packed_numel(lib, n, k), dtype=torch.int8, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_pack_weight(_ptr(qd), n, k, _ptr(qp), _stream(dev))
+    check(rc, "pack")
+    return qp.to(home) if home.type != "cuda" else qp
+
+
+def unpack(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """The packed layout -> row-major int8 [N, K] (same device as ``qp``)."""
+    home = qp.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    if qp.numel() != _packed_numel(lib, n, k):
+        raise ValueError(f"packed buffer holds {qp.numel()} bytes, [{n}, {k}] needs {_packed_numel(lib, n, k)}")
+    qd = _aligned(qp.to(dev))
+    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_unpack_weight(_ptr(qd), n, k, _ptr(q), _stream(dev))
+    check(rc, "unpack")
+    return q.to(home) if home.type != "cuda" else q
+
+
+def _dequantize_packed(qp: torch.Tensor, scale: torch.Tensor, n: int, k: int, dtype: torch.dtype) -> torch.Tensor:
+    home = qp.device
+    dev = home if home.type == "cuda" else _require_gpu()
+    lib = _native.load()
+    kdt = dtype if dtype in _DTYPE_CODE else torch.float32
+    qd = _aligned(qp.to(dev))
+    sd = _aligned(scale.to(dev, dtype=torch.float32).reshape(n))
+    out = torch.empty((n, k), dtype=kdt, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_dequantize_packed(_ptr(qd), _ptr(sd), n, k, _ptr(out), _DTYPE_CODE[kdt], _stream(dev))
+    check(rc, "dequantize")
+    if kdt != dtype:
+        out = out.to(dtype)
+    return out.to(home) if home.type != "cuda" else out
+
+
+# ---------------------------------------------------------------------------
 # fused linears
 # ---------------------------------------------------------------------------
 
@@ -209,12 +309,12 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
     w0 = weights[0]
-    dev = w0.q.device
+    dev = w0.device
     if dev.type != "cuda":
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
-    k = w0.q.shape[1]
+    k = w0.shape[1]
     for w in weights:
-        if w.q.device != dev or w.q.shape[1] != k:
+        if w.device != dev or w.shape[1] != k:
             raise ValueError("linear_group: weights must share device and in_features")
     lead = x.shape[:-1]
     x2 = _check_x(x, k, dev, "linear")
@@ -223,19 +323,22 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
     outs = (LinearOut * len(weights))()
     ys, keep = [], []
     for i, (w, b) in enumerate(zip(weights, biases)):
-        n = w.q.shape[0]
+        n = w.shape[0]
         bb = _check_bias(b, n, dev, "linear")
         y = torch.empty((m, n), dtype=out_dtype, device=dev)
         q, s = w._kernel_operands()
         keep.extend([q, s, bb])
-        outs[i].q = q.data_ptr() if q.numel() else None
+        outs[i].qp = q.data_ptr() if q.numel() else None
         outs[i].scale = s.data_ptr() if s.numel() else None
         outs[i].bias = bb.data_ptr() if bb is not None else None
         outs[i].y = y.data_ptr() if y.numel() else None
         outs[i].n = n
         ys.append(y)
     with _on_device(dev):
-        rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, _stream(dev))
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws, ws_bytes = _workspace(lib, dev, stream, m, tuple(w.shape[0] for w in weights), k, False)
+        rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
+                                        ctypes.c_void_p(stream))
     check(rc, "w8a16 linear")
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
@@ -243,12 +346,12 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
 def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> torch.Tensor:
     """``F.silu(F.linear(x, gate)) * F.linear(x, up)`` in one launch
     (engine/model.py:188-190); fp32 inside, one rounding to bf16."""
-    dev = gate.q.device
-    if dev.type != "cuda" or up.q.device != dev:
+    dev = gate.device
+    if dev.type != "cuda" or up.device != dev:
         raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
-    if gate.q.shape != up.q.shape:
+    if gate.shape != up.shape:
         raise ValueError("swiglu: gate and up weights must have the same shape")
-    n, k = gate.q.shape
+    n, k = gate.shape
     lead = x.shape[:-1]
     x2 = _check_x(x, k, dev, "swiglu")
     m = x2.shape[0]
@@ -257,7 +360,10 @@ def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> t
     qu, su = up._kernel_operands()
     lib = _native.load()
     with _on_device(dev):
-        rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, _stream(dev))
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, True)
+        rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, ws, ws_bytes,
+                                  ctypes.c_void_p(stream))
     check(rc, "w8a16 swiglu")
     return act.reshape(*lead, n)
 
@@ -273,48 +379,72 @@ def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "
 # ---------------------------------------------------------------------------
 
 class QuantizedWeight:
-    """Drop-in replacement for a plain weight tensor: stores int8 + scale
-    (engine/quantization.py:30-50).  ``get()`` gives a tensor that behaves as
-    the dequantized weight; ``F.linear`` on it runs the fused W8A16 kernel."""
+    """Drop-in replacement for a plain weight tensor: stores int8 + scale,
+    dequantizes on access (engine/quantization.py:30-50).
+
+    Storage is the packed tile layout the kernels stream (``qp``, one byte per
+    weight plus zero padding to 16 rows x 64 columns).  ``q`` gives the
+    reference's row-major int8 view, rebuilt on access by the unpack kernel
+    (bit-identical to ``quantize_per_channel(weight)[0]``); assigning ``q``
+    repacks it.  ``get()`` gives a tensor that behaves as the dequantized
+    weight; ``F.linear`` on it runs the fused W8A16 kernel.
+    """
 
     def __init__(self, weight: torch.Tensor):
+        if not isinstance(weight, torch.Tensor) or weight.dim() != 2:
+            raise ValueError("weight must be a 2-D tensor (out_features, in_features)")
+        if weight.shape[1] == 0 and weight.shape[0] > 0:
+            raise RuntimeError("amax(): Expected reduction dim 1 to have non-zero size.")
         self.dtype = weight.dtype
-        self.q, self.scale = quantize_per_channel(weight)
+        self.shape = torch.Size(weight.shape)
+        qp, scale = _quantize_packed(weight)
+        if weight.device.type != "cuda":
+            qp, scale = qp.to(weight.device), scale.to(weight.device)
+        self.qp, self.scale = qp, scale
+
+    @property
+    def q(self) -> torch.Tensor:
+        return unpack(self.qp, *self.shape)
+
+    @q.setter
+    def q(self, value: torch.Tensor) -> None:
+        self.qp = pack(value)
+        self.shape = torch.Size(value.shape)
+
+    @property
+    def device(self) -> torch.device:
+        return self.qp.device
 
     def get(self) -> torch.Tensor:
-        if self.q.device.type == "cuda":
+        if self.qp.device.type == "cuda":
             return W8A16Weight(self)
-        return dequantize(self.q, self.scale, self.dtype)
+        return self.dense()
 
     def to(self, device) -> "QuantizedWeight":
-        self.q = self.q.to(device)
+        self.qp = self.qp.to(device)
         self.scale = self.scale.to(device)
         return self
 
     @property
     def storage_bytes(self) -> int:
-        return self.q.numel() * self.q.element_size() + self.scale.numel() * self.scale.element_size()
-
-    @property
-    def shape(self) -> torch.Size:
-        return self.q.shape
+        return self.qp.numel() * self.qp.element_size() + self.scale.numel() * self.scale.element_size()
 
     def dense(self) -> torch.Tensor:
         """The reference's ``get()``: the dequantized weight in ``self.dtype``."""
-        return dequantize(self.q, self.scale, self.dtype)
+        return _dequantize_packed(self.qp, self.scale, *self.shape, self.dtype)
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
         return linear(x, self, bias, out_dtype=out_dtype)
 
     def _kernel_operands(self) -> tuple[torch.Tensor, torch.Tensor]:
-        q = self.q
-        if not q.is_contiguous() or (q.numel() and q.data_ptr() % 16):
-            q = _aligned(q)
+        qp = self.qp
+        if not qp.is_contiguous() or (qp.numel() and qp.data_ptr() % 16):
+            qp = _aligned(qp)
         s = self.scale.reshape(-1)
         if s.dtype != torch.float32 or not s.is_contiguous():
             s = s.to(torch.float32).contiguous()
-        return q, s
+        return qp, s
 
 
 class W8A16Weight(torch.Tensor):
@@ -332,7 +462,7 @@ class W8A16Weight(torch.Tensor):
     @staticmethod
     def __new__(cls, qw: QuantizedWeight):
         t = torch.Tensor._make_wrapper_subclass(
-            cls, tuple(qw.q.shape), dtype=qw.dtype, device=qw.q.device, requires_grad=False
+            cls, tuple(qw.shape), dtype=qw.dtype, device=qw.qp.device, requires_grad=False
         )
         t._qw = qw
         return t
@@ -355,7 +485,7 @@ class W8A16Weight(torch.Tensor):
             if (type(w) is W8A16Weight and type(x) is torch.Tensor
                     and (b is None or type(b) is torch.Tensor)
                     and w._qw.dtype == torch.bfloat16 and x.dtype == torch.bfloat16
-                    and x.device == w._qw.q.device):
+                    and x.device == w._qw.qp.device):
                 return w._qw.linear(x, b)
         # everything else keeps torch's own behaviour: metadata reads use the
         # wrapper's shape/dtype/device, and compute reaches __torch_dispatch__,

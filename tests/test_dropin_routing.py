@@ -22,6 +22,8 @@ class FakeQW:
 
     def __init__(self, dtype=torch.bfloat16):
         self.q = torch.randint(-127, 128, (6, 16), dtype=torch.int8)
+        self.qp = self.q  # only its device is read by the view
+        self.shape = self.q.shape
         self.scale = torch.rand(6, 1) * 0.01
         self.dtype = dtype
         self.calls = []

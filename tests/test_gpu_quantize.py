@@ -148,3 +148,41 @@ def test_quantized_weight_matches_reference_contract(gpu):
     assert (exp - act).abs().max().item() / exp.abs().max().item() < 0.05
     # .to() moves in place and returns self (engine/quantization.py:43-46)
     assert qw.to("cpu") is qw and qw.q.device.type == "cpu"
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (3, 7), (17, 100), (4864, 896), (300, 4100), (2048, 11008), (5, 2048)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_packed_storage_bit_exact(gpu, n, k, dtype):
+    """QuantizedWeight stores the packed layout: equal, byte for byte, to the
+    oracle's packing of the oracle's q; .q unpacks to the reference layout."""
+    w = random_matrix(3000 + n + k, n, k) if n >= 4 else weights(9, n, k)
+    if dtype == torch.bfloat16:
+        w = O.round_to_bf16(w)
+        wt = torch.from_numpy(O.f32_to_bf16_bits(w).view(np.int16).copy()).view(torch.bfloat16).to(gpu)
+    else:
+        wt = torch.from_numpy(w).to(gpu)
+    qw = Q.QuantizedWeight(wt)
+    q_ref, s_ref = O.quantize_per_channel(w)
+    np.testing.assert_array_equal(qw.qp.cpu().numpy(), O.pack_tiles(q_ref))
+    np.testing.assert_array_equal(qw.q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(qw.scale.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert qw.q.shape == (n, k) and qw.scale.shape == (n, 1)
+    # pack / unpack of an arbitrary row-major int8 matrix
+    r = np.random.default_rng(n).integers(-128, 128, (n, k)).astype(np.int8)
+    rp = Q.pack(torch.from_numpy(r).to(gpu))
+    np.testing.assert_array_equal(rp.cpu().numpy(), O.pack_tiles(r))
+    np.testing.assert_array_equal(Q.unpack(rp, n, k).cpu().numpy(), r)
+    # dequantize from the packed storage == the reference's dequantize
+    dense = qw.dense()
+    assert dense.dtype == dtype and dense.shape == (n, k)
+    ref = O.dequantize(q_ref, s_ref, "bf16" if dtype == torch.bfloat16 else "f32")
+    got = dense.cpu().view(torch.int16).numpy().view(np.uint16) if dtype == torch.bfloat16 else dense.cpu().numpy()
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_assigning_q_repacks(gpu):
+    qw = Q.QuantizedWeight(torch.randn(40, 96, device=gpu))
+    new = torch.randint(-127, 128, (40, 96), dtype=torch.int8, device=gpu)
+    qw.q = new
+    assert torch.equal(qw.q, new)
+    np.testing.assert_array_equal(qw.qp.cpu().numpy(), O.pack_tiles(new.cpu().numpy()))

@@ -17,7 +17,7 @@ def test_reference_api_surface():
     assert list(inspect.signature(Q.quantize_per_channel).parameters) == ["weight"]
     assert list(inspect.signature(Q.dequantize).parameters) == ["q", "scale", "dtype"]
     assert list(inspect.signature(Q.QuantizedWeight.__init__).parameters) == ["self", "weight"]
-    for attr in ("get", "to", "storage_bytes"):
+    for attr in ("get", "to", "storage_bytes", "q"):
         assert hasattr(Q.QuantizedWeight, attr)
     assert pageserve_amd.QuantizedWeight is Q.QuantizedWeight
 
@@ -55,7 +55,9 @@ def test_shape_errors_match_reference_behaviour():
 
 def test_linear_requires_a_gpu_resident_weight():
     class Fake:
-        q = torch.zeros(4, 16, dtype=torch.int8)
+        qp = torch.zeros(1024, dtype=torch.int8)
+        shape = torch.Size((4, 16))
+        device = torch.device("cpu")
         scale = torch.ones(4, 1)
 
     with pytest.raises(RuntimeError, match="ROCm GPU"):

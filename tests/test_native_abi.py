@@ -41,11 +41,18 @@ def test_abi_version_and_error_strings(native_lib):
         (lambda L: L.pgs_dequantize(None, None, 2, -3, None, 0, None), b"negative size"),
         (lambda L: L.pgs_dequantize(ctypes.c_void_p(16), ctypes.c_void_p(16), 2, 16, ctypes.c_void_p(16), 9, None),
          b"dtype"),
-        (lambda L: L.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None), b"multiple of 16"),
-        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(8), None, None, None, None, 1, 1, 4, 16, None), b"aligned"),
-        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(16), None, None, None, None, 5, 1, 4, 16, None), b"dtype"),
-        (lambda L: L.pgs_w8a16_linear_group(ctypes.c_void_p(16), None, 0, 1, 1, 16, None), b"n_outs"),
-        (lambda L: L.pgs_w8a16_swiglu(None, None, None, None, None, None, -1, 4, 16, None), b"negative size"),
+        (lambda L: L.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None, 0, None), b"multiple of 16"),
+        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(8), None, None, None, None, 1, 1, 4, 16, None, 0, None),
+         b"aligned"),
+        (lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(16), None, None, None, None, 5, 1, 4, 16, None, 0, None),
+         b"dtype"),
+        (lambda L: L.pgs_w8a16_linear_group(ctypes.c_void_p(16), None, 0, 1, 1, 16, None, 0, None), b"n_outs"),
+        (lambda L: L.pgs_w8a16_swiglu(None, None, None, None, None, None, -1, 4, 16, None, 0, None),
+         b"negative size"),
+        (lambda L: L.pgs_pack_weight(None, 4, 64, None, None), b"null pointer"),
+        (lambda L: L.pgs_unpack_weight(ctypes.c_void_p(8), 4, 64, ctypes.c_void_p(16), None), b"aligned"),
+        (lambda L: L.pgs_dequantize_packed(None, None, -1, 64, None, 0, None), b"negative size"),
+        (lambda L: L.pgs_quantize_per_channel_packed(None, 3, 4, 64, None, None, None), b"dtype"),
     ],
 )
 def test_bad_arguments_are_rejected_without_launching(native_lib, call, needle):
@@ -56,13 +63,14 @@ def test_bad_arguments_are_rejected_without_launching(native_lib, call, needle):
 
 def test_empty_problems_are_no_ops(native_lib):
     # m == 0 or n == 0: nothing to compute, success, nothing launched
-    assert native_lib.pgs_w8a16_linear(ctypes.c_void_p(256), None, None, None, None, 1, 0, 8, 64, None) == 0
+    assert native_lib.pgs_w8a16_linear(ctypes.c_void_p(256), None, None, None, None, 1, 0, 8, 64, None, 0,
+                                       None) == 0
     assert native_lib.pgs_quantize_per_channel(None, 0, 0, 64, None, None, None) == 0
     assert native_lib.pgs_dequantize(None, None, 0, 64, None, 0, None) == 0
 
 
 def test_check_raises_with_library_message(native_lib):
-    rc = native_lib.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None)
+    rc = native_lib.pgs_w8a16_linear(None, None, None, None, None, 1, 1, 4, 8, None, 0, None)
     with pytest.raises(ValueError, match="multiple of 16"):
         _native.check(rc, "w8a16 linear")
 
@@ -70,3 +78,23 @@ def test_check_raises_with_library_message(native_lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_native.NativeLibraryError, match="not found"):
         _native.load(tmp_path / "nope.so")
+
+
+def test_workspace_query(native_lib):
+    """Short-N decode shapes split K and need a workspace; wide ones do not."""
+    def need(m, ns, k, swiglu=0):
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        return native_lib.pgs_w8a16_workspace_bytes(m, arr, len(ns), k, swiglu)
+
+    assert need(1, [2048], 11008) > 0                           # down_proj at decode
+    assert need(1, [151936], 2048) == 0                         # lm_head: plenty of tiles
+    assert need(0, [2048], 2048) == 0 and need(1, [2048], -5) == 0
+    assert need(1, [0], 2048) == 0
+    assert need(4, [2048, 256, 256], 2048) >= need(4, [2048], 2048)
+
+
+@pytest.mark.parametrize("n,k,expect", [(16, 64, 1024), (17, 64, 2048), (16, 65, 2048), (0, 64, 0), (2048, 11008,
+                                                                                                    2048 * 11008),
+                                        (-1, 4, -1)])
+def test_packed_bytes(native_lib, n, k, expect):
+    assert native_lib.pgs_packed_bytes(n, k) == expect

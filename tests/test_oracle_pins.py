@@ -351,3 +351,35 @@ def test_bf16_rounding_helper_is_round_to_nearest_even():
     ours = O.f32_to_bf16_bits(v)
     theirs = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     np.testing.assert_array_equal(ours, theirs)
+
+
+# ---------------------------------------------------------------------------
+# the packed tile layout (this build's weight storage)
+# ---------------------------------------------------------------------------
+
+def test_packed_layout_lane_order():
+    """Byte 16*l + b of a block is row l%16, column 16*(l//16) + b."""
+    q = ((np.arange(16 * 64).reshape(16, 64) % 251) - 125).astype(np.int8)
+    p = O.pack_tiles(q)
+    assert p.size == 1024
+    for lane in range(64):
+        np.testing.assert_array_equal(p[16 * lane:16 * lane + 16], q[lane % 16, 16 * (lane // 16):16 * (lane // 16) + 16])
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (16, 64), (17, 65), (37, 150), (32, 128), (5, 2048)])
+def test_packed_layout_round_trip_and_padding(n, k):
+    q = np.random.default_rng(n * k).integers(-127, 128, (n, k)).astype(np.int8)
+    p = O.pack_tiles(q)
+    assert p.size == -(-n // 16) * -(-k // 64) * 1024
+    np.testing.assert_array_equal(O.unpack_tiles(p, n, k), q)
+    # block order: block (tr, tc) starts at (tr * ceil(k/64) + tc) KiB
+    tk = -(-k // 64)
+    for (r, j) in [(0, 0), (n - 1, k - 1), (n // 2, k // 3)]:
+        off = ((r // 16) * tk + j // 64) * 1024 + ((r % 16) + 16 * ((j % 64) // 16)) * 16 + j % 16
+        assert p[off] == q[r, j]
+    # padding bytes are zero: everything not covered by a real element
+    covered = np.zeros(p.size, dtype=bool)
+    for r in range(n):
+        for j in range(k):
+            covered[((r // 16) * tk + j // 64) * 1024 + ((r % 16) + 16 * ((j % 64) // 16)) * 16 + j % 16] = True
+    assert (p[~covered] == 0).all() and covered.sum() == n * k
