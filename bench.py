@@ -274,7 +274,7 @@ def main():
             proof = kernel_roofline(layers, lambda L: Q.swiglu(px, L["gate"], L["up"]),
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
-            proof["kernel"] = "gemm_kernel<128,128,NMAT=2> (fused gate|up)"
+            proof["kernel"] = "gemm_kernel<BM=64,BN=128,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
             result["prefill"] = {"m": pm, "value": round(tflops, 2), "unit": "TFLOP/s",
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                                  "ms_per_step": round(ms, 5), "flops_per_step": nflops, "steps": psteps,

@@ -28,14 +28,28 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
+// Signed byte B of v as fp32, one VALU instruction: v_cvt_f32_i32 with an
+// SDWA source selecting and sign-extending the byte.  (Left to itself the
+// compiler extracts bytes 1 and 3 with an extra 16-bit shift each.)
+template <int B>
+__device__ __forceinline__ float sbyte_to_f32(uint32_t v) {
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(v));
+  else if constexpr (B == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(v));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // 8 signed bytes (two dwords) -> 8 bf16, exact (|q| <= 127 fits bf16's 8-bit
-// significand).  Compiles to 8 v_cvt_f32_i32 with SDWA byte sign-extension
-// plus 4 v_cvt_pk_bf16_f32.
+// significand): 8 SDWA conversions + 4 v_cvt_pk_bf16_f32 (1.5 VALU/element).
 __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  f32x8 f = {(float)(int8_t)(lo), (float)(int8_t)(lo >> 8),
-             (float)(int8_t)(lo >> 16), (float)(int8_t)(lo >> 24),
-             (float)(int8_t)(hi), (float)(int8_t)(hi >> 8),
-             (float)(int8_t)(hi >> 16), (float)(int8_t)(hi >> 24)};
+  f32x8 f = {sbyte_to_f32<0>(lo), sbyte_to_f32<1>(lo), sbyte_to_f32<2>(lo), sbyte_to_f32<3>(lo),
+             sbyte_to_f32<0>(hi), sbyte_to_f32<1>(hi), sbyte_to_f32<2>(hi), sbyte_to_f32<3>(hi)};
   return __builtin_convertvector(f, bf16x8);
 }
 

@@ -1,126 +1,135 @@
-// LDS-tiled W8A16 MFMA GEMM for prefill-sized inputs (m > 16 tokens).
+// W8A16 MFMA GEMM for prefill-sized inputs (m > 16 tokens).
 //
-// 128x128 output tiles (tokens x weight rows), BK = 64, 4 waves (2 x 2), each
-// wave 64x64 via v_mfma_f32_16x16x32_bf16.  Activation tiles are copied to
-// LDS; int8 weight tiles are widened to bf16 on their way into LDS (each
-// weight converted once per workgroup).  LDS is double buffered with register
-// prefetch of the next K step, and 16-byte chunks are XOR-swizzled by row so
-// the MFMA operand reads do not conflict on banks.  Workgroup ids are
-// remapped so that the tiles sharing a weight panel run on the same XCD
-// (dispatch is round robin over the 8 XCDs, each with its own L2).  NMAT = 2
-// is the fused SwiGLU pair: gate and up tiles accumulate side by side and the
-// epilogue writes silu(g * s_g) * (u * s_u).
-#include <atomic>
+// Output tile BM tokens x BN weight rows per workgroup of 4 waves, K stepped
+// 64 at a time (one packed weight block column).  The waves split the tile
+// along N: wave w owns weight rows [w*BN/4, (w+1)*BN/4) for all BM tokens.
+//
+//  * Weights never touch LDS.  In the packed layout (pgs_common.h) a 16-row x
+//    64-k block is one contiguous KiB whose lane-l 16 bytes are exactly lane
+//    l's A operand for two v_mfma_f32_16x16x32_bf16, so each wave loads its
+//    own blocks with 128-bit loads straight into registers and widens them to
+//    bf16 there; every weight is read and converted once per workgroup.
+//  * Activations go through LDS, double buffered: [BM][64] bf16 per stage,
+//    16-byte chunks XOR-swizzled with (row/2)%8 so that the 16 lanes of a
+//    ds_read_b128 cover all 64 banks once.  All 4 waves read them as B.
+//  * Global loads run ahead of the MFMAs: one K step (LEAD = 1, predicated)
+//    or two (LEAD = 2, rotating register sets).  Weights stay in registers,
+//    activations go registers -> LDS one step before their use.
+//  * Weight loads are ordinary cached loads: the tiles_m workgroups of one
+//    weight panel run together on one XCD and share it through its L2.
+//  * NMAT = 2 is the SwiGLU pair: gate and up blocks of the same rows are
+//    accumulated side by side; the epilogue writes silu(g*s_g) * (u*s_u).
+//  * Split K: with few output tiles (o_proj / down_proj at prefill sizes) the
+//    K range is split over `splits` workgroups per tile; each writes its fp32
+//    partial tile to the workspace and a second kernel sums the partials in
+//    split order and runs the epilogue (a fixed order: reproducible).
+//  * Workgroup ids are remapped so the units sharing a weight panel (same
+//    weight rows and K split) run on the same XCD (dispatch is round robin
+//    over the 8 XCDs, each with its own L2).
+#include <type_traits>
 
 #include "pgs_linear.h"
 
 namespace pgs {
 namespace {
 
-// ===========================================================================
-// tile GEMM, m > 16
-// ===========================================================================
+constexpr int kBK = 64;
+constexpr int kBN = 128;  // weight rows per tile and matrix: 4 waves x 32
+constexpr int kThreads = 256;
 
-constexpr int kBK = 64;          // k per LDS stage: 128 bytes of bf16 per row
-constexpr int kGemmThreads = 256;  // 4 waves, 2 (m) x 2 (n)
-
-// Maps the dispatch-order workgroup id to a logical tile so that each XCD
-// (which receives ids xcd, xcd + 8, ...) gets one contiguous run of tiles.
 __device__ __forceinline__ int xcd_remap(int b, int total) {
   const int xcd = b & 7, slot = b >> 3;
   const int per = total >> 3, rem = total & 7;
   return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
-// LDS element offset (bf16 units) of logical 16-byte chunk `ch` of row `row`
-// in a [rows][64] tile; chunks are XOR-swizzled with the row's low 3 bits.
-__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ (row & 7)) << 3); }
+// element offset (bf16 units) of 16-byte chunk `ch` of row `row` in a [rows][64] stage
+__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ ((row >> 1) & 7)) << 3); }
 
-template <int BM, int BN, int NMAT, bool OUT_F32>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
-                                                            int K, int tiles_m, int tiles_total) {
-  constexpr int XS = BM * kBK;  // bf16 elements of one X stage
-  constexpr int WS = BN * kBK;  // bf16 elements of one W stage (per matrix)
-  constexpr int STAGE = XS + NMAT * WS;
-  constexpr int XL = BM / 32;   // 16-byte X chunk loads per thread
-  constexpr int WL = BN / 64;   // 16-byte int8 W loads per thread per matrix
-  constexpr int TM = BM / 32;   // 16-token MFMA tiles per wave
-  constexpr int TN = BN / 32;   // 16-row MFMA tiles per wave
-  static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
+struct GemmArgs {
+  GroupArgs g;
+  int M, K;
+  int tiles_m;     // token tiles
+  int tiles;       // output tiles (tiles_m x weight-row tiles over all members)
+  int splits;
+  float* partials;
+};
 
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
+  constexpr int TM = BM / 16;        // token tiles per wave
+  constexpr int TN = BN / 64;        // 16-row weight tiles per wave (per matrix)
+  constexpr int XS = BM * kBK;       // bf16 elements of one activation stage
+  constexpr int XL = BM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
+  static_assert(BM % 32 == 0 && BN % 64 == 0 && XL >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][XS];
 
+  const GroupArgs& a = ga.g;
+  const int M = ga.M, K = ga.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  // work unit u = (weight-row tile, split, token tile), token tile fastest:
+  // the tiles_m units that read the same weight blocks are consecutive, and
+  // the remap puts consecutive units on one XCD (one L2)
+  const int u = xcd_remap(blockIdx.x, ga.tiles * ga.splits);
+  const int tm = u % ga.tiles_m, r = u / ga.tiles_m;
+  const int s = r % ga.splits;
+  const int t = (r / ga.splits) * ga.tiles_m + tm;
 
-  const int t = xcd_remap(blockIdx.x, tiles_total);
-  // locate the group member owning this tile (units are counted in tiles)
+  // tile -> (member, n0, m0); members are counted in n-tiles of BN rows
   int g = 0;
 #pragma unroll
-  for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (i < a.n_outs && t >= a.unit_begin[i] * tiles_m && NMAT == 1) ? i : g;
-  const int tl = t - pick(a.unit_begin, g) * tiles_m;
+  for (int i = 1; i < PGS_MAX_GROUP; ++i)
+    g = (NMAT == 1 && i < a.n_outs && t >= a.unit_begin[i] * ga.tiles_m) ? i : g;
+  const int tl = t - pick(a.unit_begin, g) * ga.tiles_m;
   const int N = pick(a.n, g);
-  const int n0 = (tl / tiles_m) * BN;
-  const int m0 = (tl % tiles_m) * BM;
+  const int n0 = (tl / ga.tiles_m) * BN;
+  const int m0 = (tl % ga.tiles_m) * BM;
 
-  // global source pointers of this thread's chunks
-  const uint16_t* xsrc[XL];
-  int xoff[XL];
+  const int kb = (K + kBK - 1) / kBK;  // packed block columns = K steps
+  const int kt0 = static_cast<int>(static_cast<int64_t>(s) * kb / ga.splits);
+  const int kt1 = static_cast<int>(static_cast<int64_t>(s + 1) * kb / ga.splits);
+
+  // this wave's weight blocks: rows n0 + wave*BN/4 + nt*16 .. +15 (clamped to the
+  // last real block; rows past N are padding zeros or discarded)
+  const int last_blk = (N + 15) / 16 - 1;
+  const int8_t* wptr[NMAT][TN];
 #pragma unroll
-  for (int i = 0; i < XL; ++i) {
-    const int ci = tid + kGemmThreads * i;
-    const int row = ci >> 3, ch = ci & 7;
-    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + ch * 8;
-    xoff[i] = swz(row, ch);
-  }
-  // packed weights: thread ci reads lane (ci % 64) of 16-row block (ci / 64),
-  // i.e. row 16*(ci/64) + ci%16, k bytes 16*((ci%64)/16) .. +15 of the step
-  const int kb = (K + kBK - 1) / kBK;
-  const int last_block = (N + 15) / 16 - 1;
-  const int8_t* wsrc[NMAT][WL];
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick(a.q, g);
 #pragma unroll
-  for (int i = 0; i < WL; ++i) {
-    const int ci = tid + kGemmThreads * i;
-    const int blk = min((n0 >> 4) + (ci >> 6), last_block);
-#pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) {
-      const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick(a.q, g);
-      wsrc[mat][i] = qg + static_cast<int64_t>(blk) * kb * 1024 + (ci & 63) * 16;
+    for (int nt = 0; nt < TN; ++nt) {
+      const int blk = min((n0 >> 4) + wave * TN + nt, last_blk);
+      wptr[mat][nt] = qg + static_cast<int64_t>(blk) * kb * 1024 + lane * 16;
     }
   }
-  u32x4 xr[XL];
-  u32x4 wr[NMAT][WL];
-  const int ktiles = (K + kBK - 1) / kBK;
+  // this thread's activation chunks: row ci/8, chunk ci%8 of the stage
+  const uint16_t* xptr[XL];
+  int xoff[XL], xcol[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int ci = tid + kThreads * i;
+    const int row = ci >> 3, ch = ci & 7;
+    xptr[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + ch * 8;
+    xoff[i] = swz(row, ch);
+    xcol[i] = ch * 8;
+  }
 
-  auto gload = [&](int kt) {
+  using WRegs = u32x4[NMAT][TN];
+  using XRegs = u32x4[XL];
+  auto wload = [&](int kt, WRegs& w) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) w[mat][nt] = ld16(wptr[mat][nt] + kt * 1024);
+  };
+  // K tail: an activation chunk past K is zeroed when it is stored to LDS
+  // (masking the loaded value would wait for the load right away)
+  auto xstore = [&](uint16_t* stage, const XRegs& xv, int kt) {
     const int k0 = kt * kBK;
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      const int ci = tid + kGemmThreads * i;
-      const bool on = k0 + (ci & 7) * 8 < K;
-      xr[i] = on ? ld16(xsrc[i] + k0) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < WL; ++i) {
-#pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) wr[mat][i] = ld16(wsrc[mat][i] + kt * 1024);
-    }
-  };
-  auto lstore = [&](int stage) {
-    uint16_t* s = smem + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(s + xoff[i]) = xr[i];
-#pragma unroll
-    for (int i = 0; i < WL; ++i) {
-      const int ci = tid + kGemmThreads * i;
-      const int row = ((ci >> 6) << 4) + (ci & 15), c4 = (ci & 63) >> 4;
-#pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) {
-        uint16_t* ws = s + XS + mat * WS;
-        const u32x4 w = wr[mat][i];
-        *reinterpret_cast<bf16x8*>(ws + swz(row, 2 * c4)) = i8x8_to_bf16x8(w[0], w[1]);
-        *reinterpret_cast<bf16x8*>(ws + swz(row, 2 * c4 + 1)) = i8x8_to_bf16x8(w[2], w[3]);
-      }
+      const uint32_t mask = (k0 + xcol[i] < K) ? 0xffffffffu : 0u;
+      *reinterpret_cast<u32x4*>(stage + xoff[i]) = xv[i] & mask;
     }
   };
 
@@ -132,50 +141,136 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
 #pragma unroll
       for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
   const int lr = lane & 15, lg = lane >> 4;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) gload(kt + 1);
-    const uint16_t* s = smem + cur * STAGE;
+  auto compute = [&](const WRegs& wc, const uint16_t* stage) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int ch = 4 * h + lg;
-      bf16x8 bx[TM];
+      bf16x8 aw[NMAT][TN];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+          aw[mat][nt] = i8x8_to_bf16x8(wc[mat][nt][2 * h], wc[mat][nt][2 * h + 1]);
+      // the packed A operand of lane group lg holds k = 16*lg + 8*h .. +7:
+      // the matching activation chunk (8 bf16) is 2*lg + h
+      const int ch = 2 * lg + h;
 #pragma unroll
       for (int mt = 0; mt < TM; ++mt) {
-        const int row = wm * (BM / 2) + mt * 16 + lr;
-        bx[mt] = *reinterpret_cast<const bf16x8*>(s + swz(row, ch));
-      }
+        const bf16x8 bx = *reinterpret_cast<const bf16x8*>(stage + swz(mt * 16 + lr, ch));
 #pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) {
-        const uint16_t* ws = s + XS + mat * WS;
+        for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-        for (int nt = 0; nt < TN; ++nt) {
-          const int row = wn * (BN / 2) + nt * 16 + lr;
-          const bf16x8 aw = *reinterpret_cast<const bf16x8*>(ws + swz(row, ch));
-#pragma unroll
-          for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] = mfma16x16x32(aw, bx[mt], acc[mat][nt][mt]);
-        }
+          for (int nt = 0; nt < TN; ++nt) acc[mat][nt][mt] = mfma16x16x32(aw[mat][nt], bx, acc[mat][nt][mt]);
       }
     }
-    if (kt + 1 < ktiles) lstore(cur ^ 1);
+  };
+
+  if constexpr (LEAD == 1) {
+    // One-step prefetch, predicated: step kt + 1's loads are issued before
+    // step kt's MFMAs and land in LDS (activations) / registers (weights)
+    // after them.
+    WRegs wa, wc;
+    XRegs xa;
+    auto xload = [&](int kt) {
+      const int k0 = kt * kBK;
+#pragma unroll
+      for (int i = 0; i < XL; ++i) xa[i] = (k0 + xcol[i] < K) ? ld16(xptr[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+    };
+    if (kt0 < kt1) {
+      wload(kt0, wa);
+      xload(kt0);
+      xstore(xs[0], xa, kt0);
+    }
     __syncthreads();
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const int cur = (kt - kt0) & 1;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) wc[mat][nt] = wa[mat][nt];
+      if (kt + 1 < kt1) {
+        wload(kt + 1, wa);
+        xload(kt + 1);
+      }
+      compute(wc, xs[cur]);
+      if (kt + 1 < kt1) xstore(xs[cur ^ 1], xa, kt + 1);
+      __syncthreads();
+    }
+  } else {
+    // Two-step lead in rotating register sets (no copies): weights in three
+    // sets, activations in two (they reach LDS one step before their use).
+    // The loop is unrolled by six so every set index is static.  Loads past
+    // the end of the range are clamped to the last step (redundant, in
+    // bounds): a branch around them would make the compiler wait for every
+    // outstanding load where the paths join.  For the same reason an
+    // activation chunk past K reloads the row's first 8 columns (in bounds)
+    // and xstore zeroes it.  Activation loads are issued
+    // before weight loads, so the wait before their LDS store leaves the
+    // younger weight loads in flight.
+    WRegs wset[3];
+    XRegs xset[2];
+    const int last = kt1 - 1;
+    auto xload = [&](int kt, XRegs& xv) {
+      const int k0 = kt * kBK;
+#pragma unroll
+      for (int i = 0; i < XL; ++i) xv[i] = ld16(xptr[i] + (k0 + xcol[i] < K ? k0 : -xcol[i]));
+    };
+    auto step = [&](auto I, int kt) {
+      constexpr int i = decltype(I)::value;
+      xload(min(kt + 2, last), xset[i % 2]);
+      wload(min(kt + 2, last), wset[(i + 2) % 3]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+      compute(wset[i % 3], xs[(kt - kt0) & 1]);
+      // step kt + 1's activations were loaded one step ago
+      if (kt + 1 < kt1) xstore(xs[(kt - kt0 + 1) & 1], xset[(i + 1) % 2], kt + 1);
+      __syncthreads();
+    };
+    if (kt0 < kt1) {
+      xload(kt0, xset[0]);
+      wload(kt0, wset[0]);
+      xload(min(kt0 + 1, last), xset[1]);
+      wload(min(kt0 + 1, last), wset[1]);
+      xstore(xs[0], xset[0], kt0);
+      __syncthreads();
+      for (int kt = kt0;;) {
+        step(std::integral_constant<int, 0>{}, kt);
+        if (++kt >= kt1) break;
+        step(std::integral_constant<int, 1>{}, kt);
+        if (++kt >= kt1) break;
+        step(std::integral_constant<int, 2>{}, kt);
+        if (++kt >= kt1) break;
+        step(std::integral_constant<int, 3>{}, kt);
+        if (++kt >= kt1) break;
+        step(std::integral_constant<int, 4>{}, kt);
+        if (++kt >= kt1) break;
+        step(std::integral_constant<int, 5>{}, kt);
+        if (++kt >= kt1) break;
+      }
+    }
   }
 
-  // epilogue: lane holds rows n = base + 4*lg + r, token m = base + lr
+  // ---- epilogue: lane holds rows nb + r (r = 0..3) for token m0 + mt*16 + lr
+  if (ga.splits > 1) {
+    // partial tile in lane order: [tile][split][mat][nt][mt][lane] x f32x4
+    constexpr int SLOTS = 4 * TN * TM * 64;
+    f32x4* part = reinterpret_cast<f32x4*>(ga.partials) + (static_cast<int64_t>(t) * ga.splits + s) * NMAT * SLOTS;
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < TM; ++mt)
+          part[mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+    return;
+  }
   const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
-  const float* sc1 = a.scale[1];
+  const float* sc1 = a.scale[NMAT - 1];
   const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
   void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
-  // 4 consecutive outputs per lane: vector store when every row start is aligned
   const bool yvec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
 #pragma unroll
   for (int nt = 0; nt < TN; ++nt) {
-    const int nb = n0 + wn * (BN / 2) + nt * 16 + 4 * lg;
+    const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * lg;
     float s0[4], s1[4], bv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -186,24 +281,23 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
     }
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt) {
-      const int m = m0 + wm * (BM / 2) + mt * 16 + lr;
+      const int m = m0 + mt * 16 + lr;
       if (m >= M) continue;
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if constexpr (NMAT == 2)
-          v[r] = silu_f32(acc[0][nt][mt][r] * s0[r]) * (acc[1][nt][mt][r] * s1[r]);
+          v[r] = silu_f32(acc[0][nt][mt][r] * s0[r]) * (acc[NMAT - 1][nt][mt][r] * s1[r]);
         else
           v[r] = acc[0][nt][mt][r] * s0[r] + bv[r];
       }
       const int64_t base = static_cast<int64_t>(m) * N + nb;
       if (yvec && nb + 3 < N) {
-        if constexpr (OUT_F32) {
+        if constexpr (OUT_F32)
           *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
-        } else {
+        else
           *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + base) =
               u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        }
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -213,61 +307,143 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
   }
 }
 
-
+// Sums the split partial tiles in split order and runs the epilogue.  One
+// thread per accumulator slot (4 consecutive output rows of one token) over
+// all tiles; partial reads are coalesced 16-byte loads.
 template <int BM, int BN, int NMAT, bool OUT_F32>
-int launch_cfg(Problem& p, const GemmPlan& plan, hipStream_t st) {
-  constexpr size_t lds = sizeof(uint16_t) * 2 * (BM * kBK + NMAT * BN * kBK);
-  // the dynamic-LDS limit is a per-function, per-device attribute: set it once per device
-  static std::atomic<uint64_t> attr_done{0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(PGS_ERR_NO_DEVICE, "w8a16 gemm: hipGetDevice failed");
-  const uint64_t bit = 1ull << (dev & 63);
-  if (!(attr_done.load(std::memory_order_acquire) & bit)) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, NMAT, OUT_F32>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess)
-      return fail(PGS_ERR_LAUNCH, "w8a16 gemm: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
-    attr_done.fetch_or(bit, std::memory_order_acq_rel);
+__global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
+  constexpr int TM = BM / 16, TN = BN / 64;
+  constexpr int SLOTS = 4 * TN * TM * 64;  // per tile and matrix
+  const GroupArgs& a = ga.g;
+  const int M = ga.M;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= static_cast<int64_t>(ga.tiles) * SLOTS) return;
+  const int t = static_cast<int>(gid / SLOTS);
+  const int slot = static_cast<int>(gid - static_cast<int64_t>(t) * SLOTS);
+  const int lane = slot & 63;
+  const int mt = (slot >> 6) % TM;
+  const int nt = (slot >> 6) / TM % TN;
+  const int wave = (slot >> 6) / (TM * TN);
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PGS_MAX_GROUP; ++i)
+    g = (NMAT == 1 && i < a.n_outs && t >= a.unit_begin[i] * ga.tiles_m) ? i : g;
+  const int tl = t - pick(a.unit_begin, g) * ga.tiles_m;
+  const int N = pick(a.n, g);
+  const int n0 = (tl / ga.tiles_m) * BN;
+  const int m0 = (tl % ga.tiles_m) * BM;
+  const int m = m0 + mt * 16 + (lane & 15);
+  const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * (lane >> 4);
+  if (m >= M) return;
+  const f32x4* part = reinterpret_cast<const f32x4*>(ga.partials) + static_cast<int64_t>(t) * ga.splits * NMAT * SLOTS;
+  f32x4 v[NMAT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < ga.splits; ++sp) v[mat] += part[(static_cast<int64_t>(sp) * NMAT + mat) * SLOTS + slot];
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, NMAT, OUT_F32>), dim3(static_cast<unsigned>(plan.tiles)),
-                     dim3(kGemmThreads), lds, st, p.x, p.args, p.m, p.k, plan.tiles_m, plan.tiles);
-  return check_launch("w8a16 gemm kernel");
+  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
+  const float* sc1 = a.scale[NMAT - 1];
+  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
+  void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = nb + r;
+    if (n >= N) continue;
+    float o;
+    if constexpr (NMAT == 2) {
+      o = silu_f32(v[0][r] * sc0[n]) * (v[NMAT - 1][r] * sc1[n]);
+    } else {
+      o = v[0][r] * sc0[n];
+      if (bias) o += bf16_bits_to_f32(bias[n]);
+    }
+    store_out<OUT_F32>(y, static_cast<int64_t>(m) * N + n, o);
+  }
+}
+
+template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
+int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, NMAT, OUT_F32, OCC, LEAD>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kThreads), 0, st, x, ga);
+  int rc = check_launch("w8a16 gemm kernel");
+  if (rc || ga.splits == 1) return rc;
+  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
+  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
+                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
+  return check_launch("w8a16 gemm reduce kernel");
+}
+
+// Measured on MI355X (Qwen2.5-3B projections, 512 and 2048 tokens): the
+// SwiGLU pair is fastest with the one-step pipeline and the compiler's own
+// register budget (3 waves per SIMD); single matrices with the two-step
+// pipeline at 4 waves per SIMD.
+template <int BM, int NMAT, bool OUT_F32>
+int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  if constexpr (NMAT == 2)
+    return launch_cfg<BM, kBN, 2, OUT_F32, 1, 1>(x, ga, st);
+  else
+    return launch_cfg<BM, kBN, 1, OUT_F32, 4, 2>(x, ga, st);
+}
+
+template <int NMAT, bool OUT_F32>
+int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hipStream_t st) {
+  return plan.bm == 32 ? launch_bm<32, NMAT, OUT_F32>(x, ga, st) : launch_bm<64, NMAT, OUT_F32>(x, ga, st);
 }
 
 }  // namespace
 
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split) {
-  (void)k;
-  (void)nmat;
-  (void)can_split;
   GemmPlan p{};
-  p.bm = 128;
-  p.bn = 128;
+  p.bn = kBN;
+  int tiles_n = 0;
+  for (int i = 0; i < members; ++i) tiles_n += (n[i] + kBN - 1) / kBN;
+  const int kb = (k + kBK - 1) / kBK;
+  auto tiles_for = [&](int bm) { return static_cast<int64_t>((m + bm - 1) / bm) * tiles_n; };
+  p.bm = m <= 32 ? 32 : 64;
+  // a single matrix with a short K and few 64-token tiles: 32-token tiles
+  // give the CUs work without splitting K
+  if (nmat == 1 && p.bm == 64 && kb <= 64 && tiles_for(64) < 256) p.bm = 32;
   p.tiles_m = (m + p.bm - 1) / p.bm;
-  p.tiles_n = 0;
-  for (int i = 0; i < members; ++i) p.tiles_n += (n[i] + p.bn - 1) / p.bn;
+  p.tiles_n = tiles_n;
   p.tiles = p.tiles_m * p.tiles_n;
   p.splits = 1;
+  // few output tiles: split K until about two workgroups per CU, keeping
+  // >= 32 K steps per split (>= 8 when there are very few tiles)
+  if (can_split) {
+    const int min_steps = p.tiles < 128 ? 8 : 32;
+    while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 512 && kb / (p.splits * 2) >= min_steps)
+      p.splits *= 2;
+  }
   return p;
 }
 
 size_t gemm_partial_bytes(const GemmPlan& p, int nmat) {
-  (void)p;
-  (void)nmat;
-  return 0;
+  if (p.splits <= 1) return 0;
+  return static_cast<size_t>(p.tiles) * p.splits * nmat * p.bm * p.bn * sizeof(float);
 }
 
 int launch_gemm(Problem& p, const GemmPlan& plan, hipStream_t st) {
+  if (plan.splits > 1 && (!p.partials || p.partial_bytes < gemm_partial_bytes(plan, p.nmat)))
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 gemm: split-K plan without a large enough workspace");
   // member boundaries in units of n-tiles
+  GemmArgs ga{};
+  ga.g = p.args;
   int units = 0;
   const int members = (p.nmat == 2) ? 1 : p.args.n_outs;
   for (int i = 0; i < members; ++i) {
-    p.args.unit_begin[i] = units;
+    ga.g.unit_begin[i] = units;
     units += (p.args.n[i] + plan.bn - 1) / plan.bn;
   }
-  for (int i = members; i <= PGS_MAX_GROUP; ++i) p.args.unit_begin[i] = units;
-  if (p.nmat == 2) return launch_cfg<128, 128, 2, false>(p, plan, st);
-  return p.out_f32 ? launch_cfg<128, 128, 1, true>(p, plan, st) : launch_cfg<128, 128, 1, false>(p, plan, st);
+  for (int i = members; i <= PGS_MAX_GROUP; ++i) ga.g.unit_begin[i] = units;
+  ga.M = p.m;
+  ga.K = p.k;
+  ga.tiles_m = plan.tiles_m;
+  ga.tiles = plan.tiles;
+  ga.splits = plan.splits;
+  ga.partials = p.partials;
+  if (p.nmat == 2) return launch_plan<2, false>(p.x, ga, plan, st);
+  return p.out_f32 ? launch_plan<1, true>(p.x, ga, plan, st) : launch_plan<1, false>(p.x, ga, plan, st);
 }
 
 }  // namespace pgs

@@ -94,16 +94,22 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int koff = (c + u) * 64;
-      const bool on = K64 || koff + kgrp * 16 < K;  // activations are not padded
+      // activations are not padded: a chunk past K reloads the first 16
+      // columns of the row (in bounds, K >= 16) and mac_batch zeroes it
+      // (branch free; masking here would wait at issue)
+      const int xo = (K64 || koff + kgrp * 16 < K) ? koff : -kgrp * 16;
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat) b.w[u][mat] = ld16_stream(wrow[mat] + (c + u) * 1024);
-      b.x[u][0] = on ? ld16(xrow + koff) : u32x4{0u, 0u, 0u, 0u};
-      b.x[u][1] = on ? ld16(xrow + koff + 8) : u32x4{0u, 0u, 0u, 0u};
+      b.x[u][0] = ld16(xrow + xo);
+      b.x[u][1] = ld16(xrow + xo + 8);
     }
   };
-  auto mac_batch = [&](const Batch& b) {
+  auto mac_batch = [&](const Batch& b, int c) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) mac(b.w[u], b.x[u][0], b.x[u][1]);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t mask = (K64 || (c + u) * 64 + kgrp * 16 < K) ? 0xffffffffu : 0u;
+      mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
+    }
   };
   constexpr int kStep = NW * U;
   int c0 = cb + wave * U;
@@ -113,11 +119,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
     while (c0 + kStep + U <= ce) {
       Batch nxt;
       load_batch(nxt, c0 + kStep);
-      mac_batch(cur);
+      mac_batch(cur, c0);
       cur = nxt;
       c0 += kStep;
     }
-    mac_batch(cur);
+    mac_batch(cur, c0);
     c0 += kStep;
   }
   // the last partial batch of this wave, one chunk at a time
@@ -127,8 +133,10 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
     u32x4 wv[NMAT];
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) wv[mat] = ld16_stream(wrow[mat] + c * 1024);
-    const u32x4 x0 = on ? ld16(xrow + koff) : u32x4{0u, 0u, 0u, 0u};
-    const u32x4 x1 = on ? ld16(xrow + koff + 8) : u32x4{0u, 0u, 0u, 0u};
+    const uint32_t mask = on ? 0xffffffffu : 0u;
+    const int xo = on ? koff : -kgrp * 16;
+    const u32x4 x0 = ld16(xrow + xo) & mask;
+    const u32x4 x1 = ld16(xrow + xo + 8) & mask;
     mac(wv, x0, x1);
   }
 

@@ -37,6 +37,9 @@ SHAPES = [
     (17, 64, 64), (31, 300, 208), (64, 2048, 2048), (100, 1000, 336), (127, 129, 2048),
     (128, 2048, 2048), (129, 256, 2048), (256, 11008, 2048), (512, 2048, 2048), (512, 2048, 11008),
     (300, 2560, 2048),
+    # K below one 64-column block and K tails on the tiled path; a split-K
+    # plan (few tiles, long K) whose last block is partial
+    (20, 48, 16), (33, 130, 32), (40, 96, 48), (40, 256, 4112), (70, 2048, 11024),
 ]
 
 
@@ -67,8 +70,10 @@ def test_fp32_output(gpu, m):
 
 @pytest.mark.parametrize("m", [1, 5, 16, 64, 512])
 def test_grouped_qkv_matches_separate_calls(gpu, m):
-    """q/k/v (engine/model.py:168-170) in one launch: each output equals the
-    single-weight kernel's output bit for bit, and the oracle within tolerance."""
+    """q/k/v (engine/model.py:168-170) in one launch: each output matches the
+    oracle and its single-weight launch within tolerance.  (Not bit for bit:
+    the K-split plan depends on the launch's total tile count, so a member
+    can be summed in a different order in the group than on its own.)"""
     k = 2048
     x = activations(7000 + m, m, k)  # seeds distinct from the weights
     xs = bf16_gpu(x, gpu)
@@ -84,8 +89,8 @@ def test_grouped_qkv_matches_separate_calls(gpu, m):
     outs = Q.linear_group(xs, ws, bt)
     for j in range(3):
         single = ws[j].linear(xs, bt[j])
-        assert torch.equal(outs[j], single), f"group member {j} differs from its single launch"
         report(to_np(outs[j]), O.linear(x, qs[j], ss[j], bs[j]), k, f"qkv[{j}] m={m}")
+        report(to_np(outs[j]), to_np(single), k, f"qkv[{j}] m={m} group vs single")
 
 
 def test_leading_dims_and_noncontiguous_input(gpu):
