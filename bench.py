@@ -25,6 +25,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -165,6 +166,105 @@ def kernel_roofline(layers, launch, bytes_per_launch, flops_per_launch, bound, r
             "algorithmic_flops_per_launch": flops_per_launch}
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic from hardware counters.  Two rocprofv3 --pmc passes (FETCH_SIZE,
+# then WRITE_SIZE, KiB per dispatch) over `--pmc-workload`; each counter is
+# scaled by bytes / reading of a plain streaming kernel of known size (a
+# float32 negation, COPY_BYTES read + COPY_BYTES written), then divided into
+# per-launch bytes by `--pmc-summary`, which writes TRAFFIC_FILE.
+# ---------------------------------------------------------------------------
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
+# summary key -> pattern on the demangled kernel name (third template
+# argument of both kernels = number of matrices: 2 is the gate|up pair)
+PMC_KERNELS = {
+    "copy": r"neg_kernel",
+    "skinny_gate_up_m1": r"skinny_kernel<\d+, \d+, 2,",
+    "gemm_gate_up_m512": r"gemm_kernel<\d+, \d+, 2,",
+}
+
+
+def pmc_workload(dev, layers_n):
+    """Known-size copy, then the fused gate|up kernel at M=1 and at M=512 once
+    per layer: the dispatches the counter passes read."""
+    from pageserve_amd import quantization as Q
+
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    layers = make_layers(dev, layers_n)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for m in (1, 512):
+        x = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+        for L in layers:
+            Q.swiglu(x, L["gate"], L["up"])
+        torch.cuda.synchronize()
+    log(f"[bench] pmc workload done: copy x3, gate|up m=1 and m=512 x {layers_n} layers")
+
+
+def _pmc_means(dirs):
+    """{counter: {key: (mean KiB per dispatch, dispatches, kernel name)}} from rocprofv3 CSV output."""
+    import csv
+    import glob
+
+    out = {}
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            vals = {}
+            with open(path, newline="") as f:
+                for row in csv.DictReader(f):
+                    name = row["Kernel_Name"]
+                    for key, pattern in PMC_KERNELS.items():
+                        if re.search(pattern, name):
+                            vals.setdefault((row["Counter_Name"], key), []).append((float(row["Counter_Value"]), name))
+            for (counter, key), v in vals.items():
+                out.setdefault(counter, {})[key] = (sum(a for a, _ in v) / len(v), len(v), v[0][1])
+    return out
+
+
+def pmc_summary(dirs, commands):
+    means = _pmc_means(dirs)
+    fetch, write = means.get("FETCH_SIZE", {}), means.get("WRITE_SIZE", {})
+    if "copy" not in fetch or "copy" not in write:
+        raise SystemExit(f"pmc summary: the copy kernel's FETCH_SIZE and WRITE_SIZE are both required "
+                         f"(found {sorted((c, k) for c in means for k in means[c])})")
+    f_fac = COPY_BYTES / (fetch["copy"][0] * 1024)
+    w_fac = COPY_BYTES / (write["copy"][0] * 1024)
+    lines = ["# HBM traffic per launch from rocprofv3 --pmc (KiB per dispatch, mean over dispatches),",
+             "# each counter scaled by the factor that maps a plain streaming kernel of known size",
+             f"# (float32 negation, {COPY_BYTES} B read + {COPY_BYTES} B written) onto its true bytes.",
+             "# commands (from the repository root):"]
+    lines += [f"#   {c}" for c in commands]
+    lines.append(f"copy fetch_kib={fetch['copy'][0]:.1f} write_kib={write['copy'][0]:.1f} "
+                 f"factor_fetch={f_fac:.4f} factor_write={w_fac:.4f}")
+    for key in PMC_KERNELS:
+        if key == "copy" or key not in fetch or key not in write:
+            continue
+        fk, n, name = fetch[key]
+        wk = write[key][0]
+        traffic = fk * 1024 * f_fac + wk * 1024 * w_fac
+        lines.append(f"{key} dispatches={n} fetch_kib={fk:.1f} write_kib={wk:.1f} "
+                     f"traffic_bytes={traffic:.0f} kernel={name}")
+    return "\n".join(lines) + "\n"
+
+
+def read_traffic(key):
+    """Per-launch HBM bytes for `key` from TRAFFIC_FILE, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if parts and parts[0] == key:
+                    kv = dict(p.split("=", 1) for p in parts[1:] if "=" in p)
+                    return int(float(kv["traffic_bytes"]))
+    except (OSError, KeyError, ValueError):
+        return None
+    return None
+
+
 def cpu_baseline(layers, m, budget_s):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference_cpu_path as R
@@ -192,7 +292,21 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for the baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the dispatches the rocprofv3 --pmc traffic passes read")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="reduce rocprofv3 --pmc output directories to the traffic summary (no GPU)")
+    ap.add_argument("--pmc-command", action="append", default=[],
+                    help="command line recorded in the traffic summary (repeatable)")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        text = pmc_summary(args.pmc_summary, args.pmc_command)
+        os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+        with open(TRAFFIC_FILE, "w") as f:
+            f.write(text)
+        print(text, end="")
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this path is measured on one GPU only; --gpus must be 1 "
@@ -208,6 +322,10 @@ def main():
     _native.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.pmc_workload:
+        with torch.inference_mode():
+            pmc_workload(dev, args.layers)
+        return
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; building {args.layers} layers of int8 weights")
     layers = make_layers(dev, args.layers)
     gen = torch.Generator(device=dev).manual_seed(99 + args.m)
@@ -243,6 +361,7 @@ def main():
             roof = kernel_roofline(layers, lambda L: Q.swiglu(x, L["gate"], L["up"]), swiglu_b,
                                    4 * m * INTER * HIDDEN, "hbm")
             roof["kernel"] = "skinny_kernel<NMAT=2> (fused gate|up, 2x[11008,2048] int8)"
+            roof["traffic"] = read_traffic("skinny_gate_up_m1") if m == 1 else None
             log(f"[bench] dominant kernel: {roof['launch_us']} us/launch, {roof['achieved']} GB/s")
             down_roof = kernel_roofline(layers, lambda L: L["down"].linear(xi), linear_bytes(m, HIDDEN, INTER),
                                         2 * m * HIDDEN * INTER, "hbm")
@@ -275,6 +394,7 @@ def main():
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
             proof["kernel"] = "gemm_kernel<BM=64,BN=128,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
+            proof["traffic"] = read_traffic("gemm_gate_up_m512") if pm == 512 else None
             result["prefill"] = {"m": pm, "value": round(tflops, 2), "unit": "TFLOP/s",
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                                  "ms_per_step": round(ms, 5), "flops_per_step": nflops, "steps": psteps,

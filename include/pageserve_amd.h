@@ -152,7 +152,9 @@ typedef struct pgs_linear_out {
 /*
  * Replaces the three F.linear calls of engine/model.py:168-170 (q, k, v
  * projections of the same normalised hidden state) with one launch.  Each
- * output is exactly what pgs_w8a16_linear would write for it.
+ * output is what pgs_w8a16_linear computes for it, up to the order of the
+ * fp32 summation over K (the K split is planned for the whole group, so a
+ * member may be split differently than on its own).
  * 1 <= n_outs <= PGS_MAX_GROUP.
  */
 int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
