@@ -55,6 +55,72 @@ struct GemmArgs {
   float* partials;
 };
 
+// Split-K partial tile in lane order: [tile][split][mat][nt][mt][lane] x f32x4
+// (the reduce kernel reads the same order).
+template <int TN, int TM, int NMAT, typename Args>
+__device__ __forceinline__ void store_partials(const f32x4 (&acc)[NMAT][TN][TM], const Args& ga, int t, int s, int wave,
+                                               int lane) {
+  constexpr int SLOTS = 4 * TN * TM * 64;
+  f32x4* part = reinterpret_cast<f32x4*>(ga.partials) + (static_cast<int64_t>(t) * ga.splits + s) * NMAT * SLOTS;
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) part[mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+}
+
+// Epilogue of one workgroup tile: lane (lr, lg) of wave `wave` holds, for
+// weight tile nt and token tile mt, rows nb + r (r = 0..3) of token
+// m0 + mt*16 + lr, nb = n0 + wave*BN/4 + nt*16 + 4*lg.  Applies scale, bias
+// or SwiGLU and stores bf16 / fp32.
+template <int BN, int TN, int TM, int NMAT, bool OUT_F32>
+__device__ __forceinline__ void store_tile(const f32x4 (&acc)[NMAT][TN][TM], const GroupArgs& a, int g, int M,
+                                           int N, int m0, int n0, int wave, int lr, int lg) {
+  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
+  const float* sc1 = a.scale[NMAT - 1];
+  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
+  void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
+  const bool yvec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt) {
+    const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * lg;
+    float s0[4], s1[4], bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = min(nb + r, N - 1);
+      s0[r] = sc0[n];
+      s1[r] = (NMAT == 2) ? sc1[n] : 0.f;
+      bv[r] = (NMAT == 1 && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
+    }
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) {
+      const int m = m0 + mt * 16 + lr;
+      if (m >= M) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (NMAT == 2)
+          v[r] = silu_f32(acc[0][nt][mt][r] * s0[r]) * (acc[NMAT - 1][nt][mt][r] * s1[r]);
+        else
+          v[r] = acc[0][nt][mt][r] * s0[r] + bv[r];
+      }
+      const int64_t base = static_cast<int64_t>(m) * N + nb;
+      if (yvec && nb + 3 < N) {
+        if constexpr (OUT_F32)
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
+        else
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + base) =
+              u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < N) store_out<OUT_F32>(y, base + r, v[r]);
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
   constexpr int TM = BM / 16;        // token tiles per wave
@@ -251,60 +317,197 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(const uint16_t* __r
 
   // ---- epilogue: lane holds rows nb + r (r = 0..3) for token m0 + mt*16 + lr
   if (ga.splits > 1) {
-    // partial tile in lane order: [tile][split][mat][nt][mt][lane] x f32x4
-    constexpr int SLOTS = 4 * TN * TM * 64;
-    f32x4* part = reinterpret_cast<f32x4*>(ga.partials) + (static_cast<int64_t>(t) * ga.splits + s) * NMAT * SLOTS;
+    store_partials<TN, TM, NMAT>(acc, ga, t, s, wave, lane);
+    return;
+  }
+  store_tile<BN, TN, TM, NMAT, OUT_F32>(acc, a, g, M, N, m0, n0, wave, lr, lg);
+}
+
+// The kernel for K % 64 == 0 (every shape of the Qwen2 family): BM tokens x
+// 128 weight rows (per matrix) per workgroup, optional K split.
+//  * A 16x16x32 MFMA leaves the vector ALU only a few cycles of its issue
+//    time, so the int8 -> bf16 widening (1.5 VALU per weight element) bounds
+//    the loop unless each widened operand feeds enough MFMAs: it feeds one
+//    per 16-token tile, BM/16 of them (BM = 128: 1.5 VALU per MFMA).
+//  * Both operands use buffer loads: K is stepped through the scalar offset
+//    (no per-step address arithmetic) and the hardware range check returns
+//    zeros for weight blocks past the matrix and activation rows past M (no
+//    clamping or masking); the loop carries no VALU beyond the widening.
+//  * Weights run two K steps ahead in three rotating register sets,
+//    activations XLEAD steps ahead through double-buffered LDS; the loop is
+//    unrolled by six so every set and stage index is static.
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+
+// Linear tile index -> (weight tile, token tile) in blocks of kGroup x kGroup
+// (partial blocks at the edges), weight-tile blocks outermost.
+constexpr int kGroup = 8;
+__device__ __forceinline__ void block_order(int t, int tiles_n, int tiles_m, int& tn, int& tm) {
+  const int per_ngroup = kGroup * tiles_m;
+  const int gn = t / per_ngroup;
+  const int gn_size = min(kGroup, tiles_n - gn * kGroup);
+  const int r = t - gn * per_ngroup;
+  const int mb = r / (gn_size * kGroup);
+  const int rem = r - mb * gn_size * kGroup;
+  tn = gn * kGroup + rem % gn_size;
+  tm = mb * kGroup + rem / gn_size;
+}
+
+// A buffer resource must live in scalar registers; values the compiler cannot
+// prove wave-uniform (pointers picked from the argument arrays) are moved
+// there explicitly.  The inputs are uniform by construction.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const void* uniform(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);  // integer clamp (no fp round trip)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), 0, uniform(n), kRsrcWord3);
+}
+
+template <int BM, int NMAT, bool OUT_F32, int XLEAD, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
+  constexpr int BN = kBN, TM = BM / 16, TN = BN / 64;
+  static_assert(BM % 32 == 0, "tile shape");
+  constexpr int XS = BM * kBK;           // bf16 elements of one activation stage
+  constexpr int XL = BM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
+
+  const GroupArgs& a = ga.g;
+  const int M = ga.M, K = ga.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Work units: (weight tile, K split, token tile).  (split, weight tile)
+  // pairs form "virtual" weight tiles, split-major, ordered in blocks of
+  // kGroup virtual weight tiles x kGroup token tiles, so the ~64 workgroups
+  // an XCD runs at once share 8 weight panels and 8 activation tiles through
+  // its L2; the remap keeps consecutive units on one XCD.
+  const int tiles_n = ga.tiles / ga.tiles_m;
+  int vn, mt_all;
+  block_order(xcd_remap(blockIdx.x, ga.tiles * ga.splits), tiles_n * ga.splits, ga.tiles_m, vn, mt_all);
+  const int s = vn / tiles_n, nt_all = vn - s * tiles_n;
+  const int t = nt_all * ga.tiles_m + mt_all;  // tile index of the split partials
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (NMAT == 1 && i < a.n_outs && nt_all >= a.unit_begin[i]) ? i : g;
+  const int N = pick(a.n, g);
+  const int n0 = (nt_all - pick(a.unit_begin, g)) * BN;
+  const int m0 = mt_all * BM;
+  const int kb = K / kBK;
+  const int kt0 = static_cast<int>(static_cast<int64_t>(s) * kb / ga.splits);
+  const int kt1 = static_cast<int>(static_cast<int64_t>(s + 1) * kb / ga.splits);
+
+  // weights: one resource per matrix starting at this tile's first row block
+  const int blk0 = n0 >> 4, blocks = (N + 15) >> 4;
+  __amdgpu_buffer_rsrc_t wres[NMAT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick(a.q, g);
+    wres[mat] = make_rsrc(qg + static_cast<int64_t>(blk0) * kb * 1024, static_cast<int64_t>(blocks - blk0) * kb * 1024);
+  }
+  int woff[TN];
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt) woff[nt] = (wave * TN + nt) * kb * 1024 + lane * 16;
+  // activations: rows m0.. of x; rows past M read as zero
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<int64_t>(M - m0) * K * 2);
+  int xoff_g[XL], xoff_s[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int ci = tid + kThreads * i;
+    const int row = ci >> 3, ch = ci & 7;
+    xoff_g[i] = row * K * 2 + ch * 16;
+    xoff_s[i] = swz(row, ch);
+  }
+  const int lr = lane & 15, lg = lane >> 4;
+  // B operand of token tile mt, K half h: swz(mt*16 + lr, 2*lg + h) = mt*1024 + swz(lr, 2*lg + h)
+  const int bofs0 = swz(lr, 2 * lg), bofs1 = swz(lr, 2 * lg + 1);
+
+  using WRegs = u32x4[NMAT][TN];
+  using XRegs = u32x4[XL];
+  WRegs wset[3];
+  XRegs xset[XLEAD];
+  auto wload = [&](int kt, WRegs& w) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-      for (int nt = 0; nt < TN; ++nt)
+      for (int nt = 0; nt < TN; ++nt) w[mat][nt] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff[nt], kt * 1024, 0);
+  };
+  auto xload = [&](int kt, XRegs& xr) {
 #pragma unroll
-        for (int mt = 0; mt < TM; ++mt)
-          part[mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+    for (int i = 0; i < XL; ++i) xr[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff_g[i], kt * (kBK * 2), 0);
+  };
+  auto xstore = [&](int stage, const XRegs& xr) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(xs + stage * XS + xoff_s[i]) = xr[i];
+  };
+
+  f32x4 acc[NMAT][TN][TM];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const WRegs& wc, int stage) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 aw[NMAT][TN];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) aw[mat][nt] = i8x8_to_bf16x8(wc[mat][nt][2 * h], wc[mat][nt][2 * h + 1]);
+      const uint16_t* bsrc = xs + stage * XS + (h ? bofs1 : bofs0);
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) {
+        const bf16x8 bx = *reinterpret_cast<const bf16x8*>(bsrc + mt * 1024);
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt) acc[mat][nt][mt] = mfma16x16x32(aw[mat][nt], bx, acc[mat][nt][mt]);
+      }
+    }
+  };
+
+  const int last = kt1 - 1;
+  // activations of step kt + XLEAD are loaded at step kt into set i % XLEAD;
+  // step kt + 1's set (loaded XLEAD - 1 steps ago) is stored to LDS after the
+  // MFMAs.  Loads past the range are clamped to its last step (redundant).
+  auto step = [&](auto I, int kt) {
+    constexpr int i = decltype(I)::value;
+    xload(min(kt + XLEAD, last), xset[i % XLEAD]);
+    wload(min(kt + 2, last), wset[(i + 2) % 3]);
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+    compute(wset[i % 3], i % 2);
+    if (kt + 1 < kt1) xstore((i + 1) % 2, xset[(i + 1) % XLEAD]);
+    __syncthreads();
+  };
+  xload(kt0, xset[0]);
+  wload(kt0, wset[0]);
+  if constexpr (XLEAD == 2) xload(min(kt0 + 1, last), xset[1]);
+  wload(min(kt0 + 1, last), wset[1]);
+  xstore(0, xset[0]);
+  __syncthreads();
+  for (int kt = kt0;;) {
+    step(std::integral_constant<int, 0>{}, kt);
+    if (++kt >= kt1) break;
+    step(std::integral_constant<int, 1>{}, kt);
+    if (++kt >= kt1) break;
+    step(std::integral_constant<int, 2>{}, kt);
+    if (++kt >= kt1) break;
+    step(std::integral_constant<int, 3>{}, kt);
+    if (++kt >= kt1) break;
+    step(std::integral_constant<int, 4>{}, kt);
+    if (++kt >= kt1) break;
+    step(std::integral_constant<int, 5>{}, kt);
+    if (++kt >= kt1) break;
+  }
+  if (ga.splits > 1) {
+    store_partials<TN, TM, NMAT>(acc, ga, t, s, wave, lane);
     return;
   }
-  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
-  const float* sc1 = a.scale[NMAT - 1];
-  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
-  void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
-  const bool yvec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
-#pragma unroll
-  for (int nt = 0; nt < TN; ++nt) {
-    const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * lg;
-    float s0[4], s1[4], bv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = min(nb + r, N - 1);
-      s0[r] = sc0[n];
-      s1[r] = (NMAT == 2) ? sc1[n] : 0.f;
-      bv[r] = (NMAT == 1 && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
-    }
-#pragma unroll
-    for (int mt = 0; mt < TM; ++mt) {
-      const int m = m0 + mt * 16 + lr;
-      if (m >= M) continue;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (NMAT == 2)
-          v[r] = silu_f32(acc[0][nt][mt][r] * s0[r]) * (acc[NMAT - 1][nt][mt][r] * s1[r]);
-        else
-          v[r] = acc[0][nt][mt][r] * s0[r] + bv[r];
-      }
-      const int64_t base = static_cast<int64_t>(m) * N + nb;
-      if (yvec && nb + 3 < N) {
-        if constexpr (OUT_F32)
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
-        else
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + base) =
-              u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < N) store_out<OUT_F32>(y, base + r, v[r]);
-      }
-    }
-  }
+  store_tile<BN, TN, TM, NMAT, OUT_F32>(acc, a, g, M, N, m0, n0, wave, lr, lg);
 }
 
 // Sums the split partial tiles in split order and runs the epilogue.  One
@@ -374,12 +577,27 @@ int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   return check_launch("w8a16 gemm reduce kernel");
 }
 
-// Measured on MI355X (Qwen2.5-3B projections, 512 and 2048 tokens): the
-// SwiGLU pair is fastest with the one-step pipeline and the compiler's own
-// register budget (3 waves per SIMD); single matrices with the two-step
-// pipeline at 4 waves per SIMD.
+template <int BM, int NMAT, bool OUT_F32, int XLEAD, int OCC>
+int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
+  hipLaunchKernelGGL((gemm_k64_kernel<BM, NMAT, OUT_F32, XLEAD, OCC>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
+                     0, st, x, ga);
+  int rc = check_launch("w8a16 gemm kernel");
+  if (rc || ga.splits == 1) return rc;
+  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * kBN / 4;
+  hipLaunchKernelGGL((gemm_reduce_kernel<BM, kBN, NMAT, OUT_F32>),
+                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
+  return check_launch("w8a16 gemm reduce kernel");
+}
+
+// Measured on MI355X (Qwen2.5-3B projections, 512 and 2048 tokens).
+// K % 64 == 0: the buffer-load kernel with a two-step activation lead; the
+// SwiGLU pair at 2 waves per SIMD, single matrices at 4.  Other K: the
+// pointer kernel (SwiGLU: one-step pipeline at the compiler's register
+// budget; single matrices: two-step pipeline at 4 waves per SIMD).
 template <int BM, int NMAT, bool OUT_F32>
 int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  if (ga.K % kBK == 0) return launch_k64<BM, NMAT, OUT_F32, 2, NMAT == 2 ? 2 : 4>(x, ga, st);
   if constexpr (NMAT == 2)
     return launch_cfg<BM, kBN, 2, OUT_F32, 1, 1>(x, ga, st);
   else
@@ -408,11 +626,11 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   p.tiles_n = tiles_n;
   p.tiles = p.tiles_m * p.tiles_n;
   p.splits = 1;
-  // few output tiles: split K until about two workgroups per CU, keeping
+  // few output tiles: split K until about four workgroups per CU, keeping
   // >= 32 K steps per split (>= 8 when there are very few tiles)
   if (can_split) {
     const int min_steps = p.tiles < 128 ? 8 : 32;
-    while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 512 && kb / (p.splits * 2) >= min_steps)
+    while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 1024 && kb / (p.splits * 2) >= min_steps)
       p.splits *= 2;
   }
   return p;
