@@ -29,15 +29,22 @@ struct Problem {
   int m, k;
   int nmat;  // 1 = linear / group, 2 = SwiGLU pair
   bool out_f32;
-  float* partials;  // split-K workspace (null: no split)
+  float* partials;  // split-K partial tiles (null: no split)
   size_t partial_bytes;
+  unsigned long long* pairs;  // zeroed pair slots (skinny two-way split), or null
 };
+
+// Workspace layout: kPairBytes of pair slots (zero before first use, left
+// zero by every call), then the split-K partial tiles.  One 8-byte slot per
+// output of a 16-row tile: 256 tiles x 16 rows x 16 tokens.
+constexpr size_t kPairBytes = 256u * 256u * 8u;
 
 // Launch plan of the skinny kernel (m <= 16).
 struct SkinnyPlan {
   int tiles;   // 16-row tiles over all members
   int nw;      // waves per workgroup (split the workgroup's K range)
   int splits;  // workgroups per tile (split K across workgroups)
+  bool pair;   // two K halves combined through pair slots (no reduce launch)
 };
 
 // Launch plan of the tile GEMM (m > 16).

@@ -37,7 +37,13 @@ size_t partial_bytes(const Plan& p, int nmat) {
   return p.skinny ? skinny_partial_bytes(p.sk, nmat) : gemm_partial_bytes(p.gm, nmat);
 }
 
-size_t workspace_bytes(const Plan& p, int nmat) { return partial_bytes(p, nmat); }
+// [pair slots][partials]: the slot region comes first whenever a workspace
+// is used at all, so the same buffer serves every call shape.
+size_t workspace_bytes(const Plan& p, int nmat) {
+  const size_t part = partial_bytes(p, nmat);
+  const bool pairs = p.skinny && p.sk.pair;
+  return (part || pairs) ? kPairBytes + part : 0;
+}
 
 int run(Problem& p, void* workspace, size_t ws_bytes, hipStream_t st) {
   const int members = (p.nmat == 2) ? 1 : p.args.n_outs;
@@ -48,8 +54,9 @@ int run(Problem& p, void* workspace, size_t ws_bytes, hipStream_t st) {
                 ws_bytes, need);
   if (need) {
     if (!aligned(workspace, 256)) return fail(PGS_ERR_MISALIGNED, "w8a16: workspace must be 256-byte aligned");
-    p.partials = reinterpret_cast<float*>(workspace);
-    p.partial_bytes = ws_bytes;
+    p.pairs = reinterpret_cast<unsigned long long*>(workspace);
+    p.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kPairBytes);
+    p.partial_bytes = ws_bytes - kPairBytes;
   }
   if (plan.skinny) {
     int tiles = 0;

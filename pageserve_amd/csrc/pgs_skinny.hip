@@ -44,7 +44,8 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 
 template <int NW, int U, int NMAT, bool OUT_F32, bool K64>
 __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
-                                                         int K, int splits, float* __restrict__ partials) {
+                                                         int K, int splits, float* __restrict__ partials,
+                                                         unsigned long long* __restrict__ pairs) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = blockIdx.x / splits;
@@ -158,7 +159,23 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
       for (int w = 0; w < NW; ++w) t += red[w][mat][ln][r];
       v[mat] = t;
     }
-    if (splits > 1) {
+    if (NMAT == 1 && pairs) {
+      // The two K halves of this tile meet in one 64-bit slot per output.
+      // The first to arrive leaves (1, its partial); the second takes it,
+      // empties the slot for the next call and finishes the output.  The data
+      // travels inside the atomic, so no fence or wait is needed, and the sum
+      // does not depend on the arrival order (fp32 addition is commutative).
+      // System scope: the two workgroups run on different XCDs, and the
+      // exchange is then performed beyond their L2s.
+      unsigned long long* slot = pairs + static_cast<int64_t>(tile) * 256 + idx;
+      const unsigned long long prev = __hip_atomic_exchange(slot, (1ull << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_SYSTEM);
+      if (prev >> 32) {
+        __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        v[0] += __uint_as_float(static_cast<uint32_t>(prev));
+        if (row0 + i < N) epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v);
+      }
+    } else if (splits > 1) {
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat) mine[mat * 256 + idx] = v[mat];
     } else if (row0 + i < N) {
@@ -194,14 +211,15 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
 template <int NW, int U, int NMAT, bool OUT_F32>
 int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * plan.splits;
+  unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
   if (p.k % 64 == 0)
     hipLaunchKernelGGL((skinny_kernel<NW, U, NMAT, OUT_F32, true>), dim3(static_cast<unsigned>(grid)), dim3(64 * NW),
-                       0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials);
+                       0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
   else
     hipLaunchKernelGGL((skinny_kernel<NW, U, NMAT, OUT_F32, false>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials);
+                       dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
   int rc = check_launch("w8a16 skinny kernel");
-  if (rc || plan.splits == 1) return rc;
+  if (rc || plan.splits == 1 || plan.pair) return rc;
   hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT_F32>), dim3(static_cast<unsigned>(plan.tiles)), dim3(256), 0, st,
                      p.args, p.m, plan.splits, p.partials);
   return check_launch("w8a16 skinny reduce kernel");
@@ -225,20 +243,29 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // model): 8 waves per workgroup with 2-chunk pipelined batches is best for
   // K = 2048; a long K (down_proj, K = 11008) over few tiles wants 16 waves
   // and a 2-way K split so that twice as many CUs stream it.
-  SkinnyPlan p{tiles, 8, 1};
+  SkinnyPlan p{tiles, 8, 1, false};
   const int chunks = (k + 63) / 64;
-  if (can_split && tiles < 256 && chunks >= 128) p.splits = 2;
+  if (can_split && tiles < 256) {
+    if (nmat == 1 && chunks >= 16) {
+      p.splits = 2;  // K halves combined through pair slots
+      p.pair = true;
+    } else if (chunks >= 128) {
+      p.splits = 2;  // SwiGLU pair: partial tiles and a reduce kernel
+    }
+  }
   const int per_wg = (chunks + p.splits - 1) / p.splits;
   p.nw = per_wg >= 64 ? 16 : per_wg >= 16 ? 8 : 4;
   return p;
 }
 
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat) {
-  return p.splits > 1 ? static_cast<size_t>(p.tiles) * p.splits * nmat * 256 * sizeof(float) : 0;
+  return (p.splits > 1 && !p.pair) ? static_cast<size_t>(p.tiles) * p.splits * nmat * 256 * sizeof(float) : 0;
 }
 
 int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
-  if (plan.splits > 1 && (!p.partials || p.partial_bytes < skinny_partial_bytes(plan, p.nmat)))
+  if (plan.pair && (!p.pairs || plan.tiles * 256 * sizeof(unsigned long long) > kPairBytes || p.nmat != 1))
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: paired split without pair slots");
+  if (plan.splits > 1 && !plan.pair && (!p.partials || p.partial_bytes < skinny_partial_bytes(plan, p.nmat)))
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: split-K plan without a large enough workspace");
   if (p.nmat == 2) return launch_nw<2, false>(p, plan, st);
   return p.out_f32 ? launch_nw<1, true>(p, plan, st) : launch_nw<1, false>(p, plan, st);

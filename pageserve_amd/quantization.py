@@ -124,7 +124,8 @@ def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, s
     ws = _workspaces.get(wkey)
     if ws is None or ws.numel() < need:
         size = max(need, 2 * ws.numel() if ws is not None else 0, 4 << 20)
-        ws = torch.empty(size, dtype=torch.uint8, device=dev)
+        # zero-filled: the leading pair slots must start empty (calls leave them empty)
+        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
         if ws.data_ptr() % 256:
             raise RuntimeError("pageserve_amd: workspace allocation is not 256-byte aligned")
         _workspaces[wkey] = ws

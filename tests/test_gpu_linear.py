@@ -118,6 +118,21 @@ def test_full_size_prefill_sampled(gpu):
     assert np.isfinite(y).all()
 
 
+def test_paired_split_leaves_the_workspace_clean(gpu):
+    """Decode shapes with few row tiles split K in two and combine the halves
+    through slots at the front of the shared workspace; each call must leave
+    them empty.  Interleave differently shaped paired calls (o, down, a
+    ragged one, 16 tokens) and repeat: every result must match the oracle."""
+    cases = [_problem(gpu, 300 + j, m, n, k) for j, (m, n, k) in
+             enumerate([(1, 2048, 2048), (1, 2048, 11008), (3, 1000, 1040), (16, 256, 2048), (1, 33, 1024)])]
+    xs = [bf16_gpu(c[3], gpu) for c in cases]
+    refs = [O.linear(c[3], c[1], c[2]) for c in cases]
+    for rep in range(3):
+        outs = [c[0].linear(x) for c, x in zip(cases, xs)]
+        for (qw, q, s, x, _), y, ref in zip(cases, outs, refs):
+            report(to_np(y), ref, x.shape[1], f"paired m={x.shape[0]} n={q.shape[0]} k={x.shape[1]} rep={rep}")
+
+
 def test_deterministic(gpu):
     qw, q, s, x, _ = _problem(gpu, 77, 512, 2048, 11008)
     xs = bf16_gpu(x, gpu)
