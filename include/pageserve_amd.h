@@ -7,12 +7,14 @@
  * none allocates device memory.  Buffers are owned by the caller.
  *
  * Workspace (linear entry points): some shapes split the reduction over K
- * across workgroups and combine the partial tiles through a caller-provided
- * device buffer.  pgs_w8a16_workspace_bytes() gives the size a call needs
- * (0 = none).  The buffer must be 256-byte aligned; its contents on entry do
- * not matter.  Calls that share a workspace must be ordered (same stream, or
- * synchronised); overlapping calls on one workspace race.  Passing NULL
- * disables the split (always correct, slower for short-N shapes).
+ * across workgroups and combine the partial results through a
+ * caller-provided device buffer.  pgs_w8a16_workspace_bytes() gives the size
+ * a call needs (0 = none).  The buffer must be 256-byte aligned and
+ * zero-filled before its first use; every call leaves it valid for the next
+ * one (its leading slots are left zeroed), so one buffer of the largest size
+ * needed can serve all calls.  Calls that share a workspace must be ordered
+ * (same stream, or synchronised); overlapping calls on one workspace race.
+ * Passing NULL disables the split (always correct, slower for short-N shapes).
  *
  * Return value: PGS_OK (0) or one of the PGS_ERR_* codes below.  A call that
  * returns an error has launched nothing.  pgs_last_error() gives a
