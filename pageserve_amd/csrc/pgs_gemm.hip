@@ -27,6 +27,7 @@
 //    weight rows and K split) run on the same XCD (dispatch is round robin
 //    over the 8 XCDs, each with its own L2).
 #include <type_traits>
+#include <utility>
 
 #include "pgs_linear.h"
 
@@ -338,6 +339,18 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(const uint16_t* __r
 //    unrolled by six so every set and stage index is static.
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 
+// Runs step(integral_constant<i>, kt) for kt = kt0 .. kt1-1 with the loop
+// body unrolled over i = 0 .. sizeof...(Is)-1; the fold stops after the step
+// that ends the range.
+template <typename Step, int... Is>
+__device__ __forceinline__ void run_steps(Step& step, int kt0, int kt1, std::integer_sequence<int, Is...>) {
+  for (int kt = kt0;;)
+    if (!((step(std::integral_constant<int, Is>{}, kt), ++kt < kt1) && ...)) break;
+}
+
+constexpr int gcd2(int a, int b) { return b ? gcd2(b, a % b) : a; }
+constexpr int lcm3(int a, int b, int c) { return a / gcd2(a, b) * b / gcd2(a / gcd2(a, b) * b, c) * c; }
+
 // Linear tile index -> (weight tile, token tile) in blocks of kGroup x kGroup
 // (partial blocks at the edges), weight-tile blocks outermost.
 constexpr int kGroup = 8;
@@ -367,17 +380,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), 0, uniform(n), kRsrcWord3);
 }
 
-template <int BM, int NMAT, bool OUT_F32, int XLEAD, int OCC>
-__global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
+//  * KG = 2 runs two groups of four waves per workgroup on alternate K steps
+//    (each group with its own LDS stages), so a workgroup of a small tile
+//    still gives every SIMD two waves; group 1 hands its accumulators to
+//    group 0 through LDS at the end.  Both groups run the same number of
+//    iterations (a group past its last step loads its last step again and
+//    skips the MFMAs), so every barrier is reached by all waves.
+template <int BM, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG>
+__global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
   constexpr int BN = kBN, TM = BM / 16, TN = BN / 64;
-  static_assert(BM % 32 == 0, "tile shape");
+  constexpr int WSETS = WLEAD + 1;               // rotating weight register sets
+  constexpr int UNROLL = lcm3(WSETS, XLEAD, 2);  // static set and stage indices
+  static_assert(BM % 32 == 0 && WLEAD >= 1 && XLEAD >= 1 && (KG == 1 || KG == 2), "tile shape / pipeline");
   constexpr int XS = BM * kBK;           // bf16 elements of one activation stage
   constexpr int XL = BM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
+  constexpr int kStageBytes = KG * 2 * XS * 2;
+  constexpr int kRedBytes = KG > 1 ? 4 * NMAT * TN * TM * 64 * 16 : 0;
+  __shared__ __attribute__((aligned(16))) char smem[kStageBytes > kRedBytes ? kStageBytes : kRedBytes];
 
   const GroupArgs& a = ga.g;
   const int M = ga.M, K = ga.K;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kg = tid >> 8;
+  const int tid_g = tid & (kThreads - 1);
+  uint16_t* const xs = reinterpret_cast<uint16_t*>(smem) + kg * 2 * XS;
   // Work units: (weight tile, K split, token tile).  (split, weight tile)
   // pairs form "virtual" weight tiles, split-major, ordered in blocks of
   // kGroup virtual weight tiles x kGroup token tiles, so the ~64 workgroups
@@ -397,6 +422,12 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t*
   const int kb = K / kBK;
   const int kt0 = static_cast<int>(static_cast<int64_t>(s) * kb / ga.splits);
   const int kt1 = static_cast<int>(static_cast<int64_t>(s + 1) * kb / ga.splits);
+  // this group's K steps: kt0 + kg, kt0 + kg + KG, ... < kt1
+  // (a group with no step at all, range <= kg, only loads step kt0 and computes nothing)
+  const int range = kt1 - kt0;
+  const int iters = (range + KG - 1) / KG;
+  const int first = kt0 + kg;
+  const int last = range > kg ? kt0 + kg + ((range - 1 - kg) / KG) * KG : kt0;
 
   // weights: one resource per matrix starting at this tile's first row block
   const int blk0 = n0 >> 4, blocks = (N + 15) >> 4;
@@ -414,7 +445,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t*
   int xoff_g[XL], xoff_s[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
-    const int ci = tid + kThreads * i;
+    const int ci = tid_g + kThreads * i;
     const int row = ci >> 3, ch = ci & 7;
     xoff_g[i] = row * K * 2 + ch * 16;
     xoff_s[i] = swz(row, ch);
@@ -425,7 +456,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t*
 
   using WRegs = u32x4[NMAT][TN];
   using XRegs = u32x4[XL];
-  WRegs wset[3];
+  WRegs wset[WSETS];
   XRegs xset[XLEAD];
   auto wload = [&](int kt, WRegs& w) {
 #pragma unroll
@@ -470,38 +501,50 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t*
     }
   };
 
-  const int last = kt1 - 1;
-  // activations of step kt + XLEAD are loaded at step kt into set i % XLEAD;
-  // step kt + 1's set (loaded XLEAD - 1 steps ago) is stored to LDS after the
-  // MFMAs.  Loads past the range are clamped to its last step (redundant).
-  auto step = [&](auto I, int kt) {
+  // Iteration j (position i of the unrolled loop) handles this group's K
+  // step kt = first + j*KG: load the weights of iteration j + WLEAD into set
+  // (i + WLEAD) % WSETS and the activations of iteration j + XLEAD into set
+  // i % XLEAD, run the MFMAs of step kt (weights in set i % WSETS,
+  // activations in LDS stage i % 2), then store iteration j + 1's activations
+  // (loaded XLEAD - 1 iterations ago, set (i + 1) % XLEAD) to the other
+  // stage.  Loads past the group's last step are clamped to it (redundant).
+  auto step = [&](auto I, int j) {
     constexpr int i = decltype(I)::value;
-    xload(min(kt + XLEAD, last), xset[i % XLEAD]);
-    wload(min(kt + 2, last), wset[(i + 2) % 3]);
+    const int kt = first + j * KG;
+    xload(min(kt + XLEAD * KG, last), xset[i % XLEAD]);
+    wload(min(kt + WLEAD * KG, last), wset[(i + WLEAD) % WSETS]);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
-    compute(wset[i % 3], i % 2);
-    if (kt + 1 < kt1) xstore((i + 1) % 2, xset[(i + 1) % XLEAD]);
+    if (KG == 1 || kt < kt1) compute(wset[i % WSETS], i % 2);
+    if (j + 1 < iters) xstore((i + 1) % 2, xset[(i + 1) % XLEAD]);
     __syncthreads();
   };
-  xload(kt0, xset[0]);
-  wload(kt0, wset[0]);
-  if constexpr (XLEAD == 2) xload(min(kt0 + 1, last), xset[1]);
-  wload(min(kt0 + 1, last), wset[1]);
+#pragma unroll
+  for (int j = 0; j < XLEAD; ++j) xload(min(first + j * KG, last), xset[j]);
+#pragma unroll
+  for (int j = 0; j < WLEAD; ++j) wload(min(first + j * KG, last), wset[j]);
   xstore(0, xset[0]);
   __syncthreads();
-  for (int kt = kt0;;) {
-    step(std::integral_constant<int, 0>{}, kt);
-    if (++kt >= kt1) break;
-    step(std::integral_constant<int, 1>{}, kt);
-    if (++kt >= kt1) break;
-    step(std::integral_constant<int, 2>{}, kt);
-    if (++kt >= kt1) break;
-    step(std::integral_constant<int, 3>{}, kt);
-    if (++kt >= kt1) break;
-    step(std::integral_constant<int, 4>{}, kt);
-    if (++kt >= kt1) break;
-    step(std::integral_constant<int, 5>{}, kt);
-    if (++kt >= kt1) break;
+  run_steps(step, 0, iters, std::make_integer_sequence<int, UNROLL>{});
+
+  if constexpr (KG > 1) {
+    // group 1's accumulators -> LDS (the stages are free after the last barrier)
+    f32x4* red = reinterpret_cast<f32x4*>(smem);
+    if (kg == 1) {
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < TM; ++mt) red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] += red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane];
   }
   if (ga.splits > 1) {
     store_partials<TN, TM, NMAT>(acc, ga, t, s, wave, lane);
@@ -509,7 +552,6 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_k64_kernel(const uint16_t*
   }
   store_tile<BN, TN, TM, NMAT, OUT_F32>(acc, a, g, M, N, m0, n0, wave, lr, lg);
 }
-
 // Sums the split partial tiles in split order and runs the epilogue.  One
 // thread per accumulator slot (4 consecutive output rows of one token) over
 // all tiles; partial reads are coalesced 16-byte loads.
@@ -577,11 +619,11 @@ int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   return check_launch("w8a16 gemm reduce kernel");
 }
 
-template <int BM, int NMAT, bool OUT_F32, int XLEAD, int OCC>
+template <int BM, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG = 1>
 int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
-  hipLaunchKernelGGL((gemm_k64_kernel<BM, NMAT, OUT_F32, XLEAD, OCC>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
-                     0, st, x, ga);
+  hipLaunchKernelGGL((gemm_k64_kernel<BM, NMAT, OUT_F32, WLEAD, XLEAD, OCC, KG>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kThreads * KG), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
   if (rc || ga.splits == 1) return rc;
   const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * kBN / 4;
@@ -591,13 +633,19 @@ int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 }
 
 // Measured on MI355X (Qwen2.5-3B projections, 512 and 2048 tokens).
-// K % 64 == 0: the buffer-load kernel with a two-step activation lead; the
-// SwiGLU pair at 2 waves per SIMD, single matrices at 4.  Other K: the
-// pointer kernel (SwiGLU: one-step pipeline at the compiler's register
-// budget; single matrices: two-step pipeline at 4 waves per SIMD).
+// K % 64 == 0: the buffer-load kernel with two-step weight and activation
+// leads; the SwiGLU pair at 2 waves per SIMD, single matrices at 4, or, with
+// at most two work units per CU (o / q|k|v / down_proj at 512 tokens), in two
+// K groups per workgroup.  Other K: the pointer kernel (SwiGLU: one-step
+// pipeline at the compiler's register budget; single matrices: two-step
+// pipeline at 4 waves per SIMD).
 template <int BM, int NMAT, bool OUT_F32>
 int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
-  if (ga.K % kBK == 0) return launch_k64<BM, NMAT, OUT_F32, 2, NMAT == 2 ? 2 : 4>(x, ga, st);
+  if (ga.K % kBK == 0) {
+    if constexpr (NMAT == 2) return launch_k64<BM, 2, OUT_F32, 2, 2, 2>(x, ga, st);
+    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 512) return launch_k64<BM, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
+    return launch_k64<BM, 1, OUT_F32, 2, 2, 4>(x, ga, st);
+  }
   if constexpr (NMAT == 2)
     return launch_cfg<BM, kBN, 2, OUT_F32, 1, 1>(x, ga, st);
   else
