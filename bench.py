@@ -175,12 +175,12 @@ def kernel_roofline(layers, launch, bytes_per_launch, flops_per_launch, bound, r
 # ---------------------------------------------------------------------------
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
-# summary key -> pattern on the demangled kernel name (third template
-# argument of both kernels = number of matrices: 2 is the gate|up pair)
+# summary key -> pattern on the demangled kernel name (the number-of-matrices
+# template argument is 2 for the gate|up pair)
 PMC_KERNELS = {
     "copy": r"neg_kernel",
     "skinny_gate_up_m1": r"skinny_kernel<\d+, \d+, 2,",
-    "gemm_gate_up_m512": r"gemm_kernel<\d+, \d+, 2,",
+    "gemm_gate_up_m512": r"gemm_k64_kernel<\d+, 2,|gemm_kernel<\d+, \d+, 2,",
 }
 
 
@@ -393,7 +393,7 @@ def main():
             proof = kernel_roofline(layers, lambda L: Q.swiglu(px, L["gate"], L["up"]),
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
-            proof["kernel"] = "gemm_kernel<BM=64,BN=128,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
+            proof["kernel"] = "gemm_k64_kernel<BM=64,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
             proof["traffic"] = read_traffic("gemm_gate_up_m512") if pm == 512 else None
             result["prefill"] = {"m": pm, "value": round(tflops, 2), "unit": "TFLOP/s",
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),

@@ -352,7 +352,9 @@ constexpr int gcd2(int a, int b) { return b ? gcd2(b, a % b) : a; }
 constexpr int lcm3(int a, int b, int c) { return a / gcd2(a, b) * b / gcd2(a / gcd2(a, b) * b, c) * c; }
 
 // Linear tile index -> (weight tile, token tile) in blocks of kGroup x kGroup
-// (partial blocks at the edges), weight-tile blocks outermost.
+// (partial blocks at the edges), weight-tile blocks outermost, token tiles
+// fastest inside a block: the units of one weight tile stay contiguous, so
+// the contiguous range each XCD receives splits at most one weight panel.
 constexpr int kGroup = 8;
 __device__ __forceinline__ void block_order(int t, int tiles_n, int tiles_m, int& tn, int& tm) {
   const int per_ngroup = kGroup * tiles_m;
@@ -360,9 +362,10 @@ __device__ __forceinline__ void block_order(int t, int tiles_n, int tiles_m, int
   const int gn_size = min(kGroup, tiles_n - gn * kGroup);
   const int r = t - gn * per_ngroup;
   const int mb = r / (gn_size * kGroup);
+  const int gm_size = min(kGroup, tiles_m - mb * kGroup);
   const int rem = r - mb * gn_size * kGroup;
-  tn = gn * kGroup + rem % gn_size;
-  tm = mb * kGroup + rem / gn_size;
+  tn = gn * kGroup + rem / gm_size;
+  tm = mb * kGroup + rem % gm_size;
 }
 
 // A buffer resource must live in scalar registers; values the compiler cannot
