@@ -389,9 +389,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 //    group 0 through LDS at the end.  Both groups run the same number of
 //    iterations (a group past its last step loads its last step again and
 //    skips the MFMAs), so every barrier is reached by all waves.
-template <int BM, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG>
+template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG>
 __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
-  constexpr int BN = kBN, TM = BM / 16, TN = BN / 64;
+  constexpr int TM = BM / 16, TN = BN / 64;
+  static_assert(BN % 64 == 0, "weight rows per tile: 4 waves x 16-row multiples");
   constexpr int WSETS = WLEAD + 1;               // rotating weight register sets
   constexpr int UNROLL = lcm3(WSETS, XLEAD, 2);  // static set and stage indices
   static_assert(BM % 32 == 0 && WLEAD >= 1 && XLEAD >= 1 && (KG == 1 || KG == 2), "tile shape / pipeline");
@@ -622,15 +623,15 @@ int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   return check_launch("w8a16 gemm reduce kernel");
 }
 
-template <int BM, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG = 1>
+template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG = 1>
 int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
-  hipLaunchKernelGGL((gemm_k64_kernel<BM, NMAT, OUT_F32, WLEAD, XLEAD, OCC, KG>), dim3(static_cast<unsigned>(grid)),
+  hipLaunchKernelGGL((gemm_k64_kernel<BM, BN, NMAT, OUT_F32, WLEAD, XLEAD, OCC, KG>), dim3(static_cast<unsigned>(grid)),
                      dim3(kThreads * KG), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
   if (rc || ga.splits == 1) return rc;
-  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * kBN / 4;
-  hipLaunchKernelGGL((gemm_reduce_kernel<BM, kBN, NMAT, OUT_F32>),
+  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
+  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
                      dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
   return check_launch("w8a16 gemm reduce kernel");
 }
@@ -645,9 +646,9 @@ int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 template <int BM, int NMAT, bool OUT_F32>
 int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   if (ga.K % kBK == 0) {
-    if constexpr (NMAT == 2) return launch_k64<BM, 2, OUT_F32, 2, 2, 2>(x, ga, st);
-    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 512) return launch_k64<BM, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
-    return launch_k64<BM, 1, OUT_F32, 2, 2, 4>(x, ga, st);
+    if constexpr (NMAT == 2) return launch_k64<BM, kBN, 2, OUT_F32, 2, 2, 2>(x, ga, st);
+    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 512) return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
+    return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 4>(x, ga, st);
   }
   if constexpr (NMAT == 2)
     return launch_cfg<BM, kBN, 2, OUT_F32, 1, 1>(x, ga, st);
@@ -657,6 +658,11 @@ int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 
 template <int NMAT, bool OUT_F32>
 int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hipStream_t st) {
+  // the SwiGLU pair at more than 64 tokens: 128 tokens x 64 rows per matrix
+  // (each widened weight operand feeds 8 MFMAs; B operands are reused across
+  // the pair's two A tiles per wave)
+  if constexpr (NMAT == 2)
+    if (plan.bm == 128) return launch_k64<128, 64, 2, OUT_F32, 2, 1, 2>(x, ga, st);
   return plan.bm == 32 ? launch_bm<32, NMAT, OUT_F32>(x, ga, st) : launch_bm<64, NMAT, OUT_F32>(x, ga, st);
 }
 
@@ -664,12 +670,12 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
 
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split) {
   GemmPlan p{};
-  p.bn = kBN;
+  p.bn = (nmat == 2 && m > 64 && k % kBK == 0) ? 64 : kBN;
   int tiles_n = 0;
-  for (int i = 0; i < members; ++i) tiles_n += (n[i] + kBN - 1) / kBN;
+  for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
   const int kb = (k + kBK - 1) / kBK;
   auto tiles_for = [&](int bm) { return static_cast<int64_t>((m + bm - 1) / bm) * tiles_n; };
-  p.bm = m <= 32 ? 32 : 64;
+  p.bm = p.bn == 64 ? 128 : m <= 32 ? 32 : 64;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K
   if (nmat == 1 && p.bm == 64 && kb <= 64 && tiles_for(64) < 256) p.bm = 32;

@@ -29,7 +29,9 @@ def _mlp_weights(gpu, seed, inter, hidden):
 @pytest.mark.parametrize("m,inter,hidden", [(1, 11008, 2048), (4, 11008, 2048), (16, 11008, 2048),
                                             (17, 11008, 2048), (128, 11008, 2048), (512, 11008, 2048),
                                             (3, 100, 48), (40, 300, 208), (20, 64, 16),
-                                            (50, 130, 48), (24, 256, 4112)])
+                                            (50, 130, 48), (24, 256, 4112),
+                                            # 128-token x 64-row tiles: split K, ragged M and N
+                                            (100, 256, 4096), (300, 1000, 2048), (65, 64, 64)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
     ws = _mlp_weights(gpu, 10 + m + inter, inter, hidden)
     x = activations(m, m, hidden)
