@@ -138,6 +138,32 @@ int pgs_w8a16_linear(const void* x, const int8_t* qp, const float* scale,
                      size_t workspace_bytes, void* stream);
 
 /*
+ * Replaces x = residual + F.linear(h, _resolve(W)) -- engine/model.py:184
+ * (o_proj) and :190 (down_proj) -- with one launch: the residual add runs in
+ * the linear's epilogue, with the reference's roundings,
+ *   y = bf16( residual + bf16( x . (q * scale)^T + bias ) )
+ * (fp32 output: y = residual + x . (q * scale)^T + bias).  residual: bf16
+ * [m, n]; y may be the residual buffer itself (in place).  Otherwise as
+ * pgs_w8a16_linear.
+ */
+int pgs_w8a16_linear_residual(const void* x, const int8_t* qp, const float* scale,
+                              const void* bias, const void* residual, void* y,
+                              int y_dtype, int64_t m, int64_t n, int64_t k,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
+ * Replaces rms_norm(x, weight, eps) -- engine/model.py:29-34, applied before
+ * the q|k|v (engine/model.py:166) and gate|up (:187) projections -- with one
+ * kernel:
+ *   r = 1 / sqrt(mean_j x[i,j]^2 + eps)   (fp32)
+ *   h[i,j] = bf16( weight[j] * bf16( x[i,j] * r ) )
+ * x, weight, h: bf16 ([m, k], [k], [m, k]); h may not alias x.
+ */
+int pgs_rmsnorm(const void* x, const void* weight, float eps, void* h,
+                int64_t m, int64_t k, void* stream);
+
+/*
  * One output of a grouped linear: several quantized weights that read the
  * same activations (the q/k/v triple of engine/model.py:168-170).
  */

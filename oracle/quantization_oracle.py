@@ -177,6 +177,34 @@ def mlp(x, q_gate, s_gate, q_up, s_up, q_down, s_down) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------
+# the linears' neighbours (engine/model.py:29-34, 166, 184, 187, 190)
+# --------------------------------------------------------------------------
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """``rms_norm(x, weight, eps)`` (engine/model.py:29-34) for bf16 tensors:
+    var = mean(x^2) over the last dim in fp32, r = rsqrt(var + eps) in fp32,
+    h = bf16(weight * bf16(x * r)).  ``x``, ``weight``: bf16-representable
+    float32 arrays.  The mean is formed in float64 and rounded once to fp32 (a
+    fp32 reduction in any order agrees with it to a few fp32 ulps); the
+    rsqrt is correctly rounded.  Returns bf16-representable float32."""
+    x = np.asarray(x, dtype=np.float32)
+    var = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float64))).astype(np.float32)
+    t = round_to_bf16((x * r).astype(np.float32))
+    return round_to_bf16((np.asarray(weight, dtype=np.float32) * t).astype(np.float32))
+
+
+def linear_residual(x, q, scale, residual, bias=None, bf16_out: bool = True) -> np.ndarray:
+    """``residual + F.linear(h, W, b)`` (engine/model.py:184, 190): the linear
+    output is rounded to the output dtype first, then added to the bf16
+    residual and rounded once more (bf16 output)."""
+    lin = linear(x, q, scale, bias)
+    if bf16_out:
+        return round_to_bf16((round_to_bf16(lin) + np.asarray(residual, dtype=np.float32)).astype(np.float32))
+    return (lin + np.asarray(residual, dtype=np.float32)).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
 # Tolerances stated by the path's specification
 # --------------------------------------------------------------------------
 

@@ -13,6 +13,7 @@ from .quantization import (  # noqa: F401
     linear_group,
     mlp,
     quantize_per_channel,
+    rmsnorm,
     swiglu,
 )
 

@@ -81,6 +81,7 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[NMAT][TN][TM], con
   const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
   const float* sc1 = a.scale[NMAT - 1];
   const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
+  const uint16_t* res = (NMAT == 2) ? nullptr : pick(a.res, g);
   void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
   const bool yvec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
 #pragma unroll
@@ -107,6 +108,10 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[NMAT][TN][TM], con
           v[r] = acc[0][nt][mt][r] * s0[r] + bv[r];
       }
       const int64_t base = static_cast<int64_t>(m) * N + nb;
+      if (NMAT == 1 && res) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = add_residual<OUT_F32>(v[r], res, base + min(r, N - 1 - nb));
+      }
       if (yvec && nb + 3 < N) {
         if constexpr (OUT_F32)
           *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
@@ -605,6 +610,7 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
     } else {
       o = v[0][r] * sc0[n];
       if (bias) o += bf16_bits_to_f32(bias[n]);
+      o = add_residual<OUT_F32>(o, pick(a.res, g), static_cast<int64_t>(m) * N + n);
     }
     store_out<OUT_F32>(y, static_cast<int64_t>(m) * N + n, o);
   }

@@ -18,6 +18,7 @@ struct GroupArgs {
   const float* scale[PGS_MAX_GROUP];
   const uint16_t* bias[PGS_MAX_GROUP];
   void* y[PGS_MAX_GROUP];
+  const uint16_t* res[PGS_MAX_GROUP];  // bf16 [m, n] residual added to the output, or null
   int32_t n[PGS_MAX_GROUP];
   int32_t unit_begin[PGS_MAX_GROUP + 1];  // first work unit (tile) of each member
   int32_t n_outs;
@@ -89,6 +90,15 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 // displacing reusable lines (activations, partials) in the caches.
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// y = residual + linear with the reference's roundings (engine/model.py:184,
+// 190): the linear output is rounded to the output type first, then added.
+template <bool OUT_F32>
+__device__ __forceinline__ float add_residual(float lin, const uint16_t* res, int64_t idx) {
+  if (!res) return lin;
+  const float l = OUT_F32 ? lin : bf16_bits_to_f32(f32_to_bf16_bits(lin));
+  return l + bf16_bits_to_f32(res[idx]);
 }
 
 template <bool OUT_F32>

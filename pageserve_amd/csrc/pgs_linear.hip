@@ -112,10 +112,12 @@ extern "C" size_t pgs_w8a16_workspace_bytes(int64_t m, const int64_t* n, int n_o
   return workspace_bytes(make_plan(static_cast<int>(m), static_cast<int>(k), nmat, nn, members, true), nmat);
 }
 
-extern "C" int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs, int n_outs, int y_dtype,
-                                      int64_t m, int64_t k, void* workspace, size_t workspace_bytes_,
-                                      void* stream) {
-  const char* fn = "pgs_w8a16_linear_group";
+namespace {
+
+// q/k/v-style group of linears on the same activations; res (null or one
+// bf16 [m, n] residual per output) is added in the epilogue.
+int linear_group_impl(const char* fn, const void* x, const pgs_linear_out* outs, const void* const* res, int n_outs,
+                      int y_dtype, int64_t m, int64_t k, void* workspace, size_t workspace_bytes_, void* stream) {
   int rc = check_common(fn, x, m, k);
   if (rc) return rc;
   if (!outs || n_outs < 1 || n_outs > PGS_MAX_GROUP)
@@ -132,11 +134,15 @@ extern "C" int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
   for (int i = 0; i < n_outs; ++i) {
     rc = check_member(fn, outs[i].qp, outs[i].scale, outs[i].bias, outs[i].y, outs[i].n, m, k);
     if (rc) return rc;
+    if (res && outs[i].n > 0 && m > 0 && !res[i])
+      return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null residual pointer", fn);
+    if (res && !aligned(res[i], 2)) return fail(PGS_ERR_MISALIGNED, "%s: residual misaligned", fn);
     if (outs[i].n == 0) continue;
     p.args.q[used] = outs[i].qp;
     p.args.scale[used] = outs[i].scale;
     p.args.bias[used] = reinterpret_cast<const uint16_t*>(outs[i].bias);
     p.args.y[used] = outs[i].y;
+    p.args.res[used] = res ? reinterpret_cast<const uint16_t*>(res[i]) : nullptr;
     p.args.n[used] = static_cast<int32_t>(outs[i].n);
     ++used;
   }
@@ -148,16 +154,35 @@ extern "C" int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs,
     p.args.scale[i] = p.args.scale[0];
     p.args.bias[i] = nullptr;
     p.args.y[i] = p.args.y[0];
+    p.args.res[i] = nullptr;
     p.args.n[i] = 0;
   }
   return run(p, workspace, workspace_bytes_, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs, int n_outs, int y_dtype,
+                                      int64_t m, int64_t k, void* workspace, size_t workspace_bytes_,
+                                      void* stream) {
+  return linear_group_impl("pgs_w8a16_linear_group", x, outs, nullptr, n_outs, y_dtype, m, k, workspace,
+                           workspace_bytes_, stream);
 }
 
 extern "C" int pgs_w8a16_linear(const void* x, const int8_t* q, const float* scale, const void* bias, void* y,
                                 int y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
                                 size_t workspace_bytes_, void* stream) {
   pgs_linear_out o{q, scale, bias, y, n};
-  return pgs_w8a16_linear_group(x, &o, 1, y_dtype, m, k, workspace, workspace_bytes_, stream);
+  return linear_group_impl("pgs_w8a16_linear", x, &o, nullptr, 1, y_dtype, m, k, workspace, workspace_bytes_, stream);
+}
+
+extern "C" int pgs_w8a16_linear_residual(const void* x, const int8_t* q, const float* scale, const void* bias,
+                                         const void* residual, void* y, int y_dtype, int64_t m, int64_t n, int64_t k,
+                                         void* workspace, size_t workspace_bytes_, void* stream) {
+  pgs_linear_out o{q, scale, bias, y, n};
+  const void* res[1] = {residual};
+  return linear_group_impl("pgs_w8a16_linear_residual", x, &o, res, 1, y_dtype, m, k, workspace, workspace_bytes_,
+                           stream);
 }
 
 extern "C" int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float* s_gate, const int8_t* q_up,

@@ -38,6 +38,7 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
     out = v[0] * sc0[n];
     const uint16_t* bias = pick(a.bias, g);
     if (bias) out += bf16_bits_to_f32(bias[n]);
+    out = add_residual<OUT_F32>(out, pick(a.res, g), static_cast<int64_t>(mm) * N + n);
   }
   store_out<OUT_F32>(y, static_cast<int64_t>(mm) * N + n, out);
 }

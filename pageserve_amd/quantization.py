@@ -47,6 +47,7 @@ __all__ = [
     "linear_group",
     "swiglu",
     "mlp",
+    "rmsnorm",
     "pack",
     "unpack",
 ]
@@ -289,13 +290,77 @@ def _check_bias(bias: torch.Tensor | None, n: int, device: torch.device, what: s
 
 
 def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
-           out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+           out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
     """``F.linear(x, dequantize(q, scale, bf16), bias)`` fused: y = x (q s)^T + b.
 
     x: bf16 [..., K] on the weight's GPU.  out_dtype: bf16 (projections) or
     fp32 (the lm_head logits).  Returns [..., N].
+
+    residual (bf16 [..., N]): returns ``residual + F.linear(x, W, b)`` with the
+    reference's roundings (engine/model.py:184, 190) from the same launch.
+    out: optional contiguous result buffer of the right shape and dtype; it
+    may be the residual itself (in place).
     """
-    return linear_group(x, [weight], [bias], out_dtype=out_dtype)[0]
+    if residual is None and out is None:
+        return linear_group(x, [weight], [bias], out_dtype=out_dtype)[0]
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
+    dev = weight.device
+    if dev.type != "cuda":
+        raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
+    n, k = weight.shape
+    lead = x.shape[:-1]
+    x2 = _check_x(x, k, dev, "linear")
+    m = x2.shape[0]
+    bb = _check_bias(bias, n, dev, "linear")
+    res = None
+    if residual is not None:
+        if residual.device != dev or residual.dtype != torch.bfloat16 or residual.shape[-1] != n \
+                or residual.numel() != m * n:
+            raise ValueError(f"linear: residual must be a bf16 [..., {n}] tensor with {m} rows on {dev}")
+        res = residual.reshape(m, n)
+        if not res.is_contiguous():
+            res = res.contiguous()
+    if out is None:
+        y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    else:
+        if out.device != dev or out.dtype != out_dtype or out.numel() != m * n or not out.is_contiguous():
+            raise ValueError(f"linear: out must be a contiguous {out_dtype} tensor of {m * n} elements on {dev}")
+        y = out.view(m, n)
+    q, s = weight._kernel_operands()
+    lib = _native.load()
+    with _on_device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, False)
+        rc = lib.pgs_w8a16_linear_residual(_ptr(x2), _ptr(q), _ptr(s), _ptr(bb), _ptr(res), _ptr(y),
+                                           _DTYPE_CODE[out_dtype], m, n, k, ws, ws_bytes, ctypes.c_void_p(stream))
+    check(rc, "w8a16 linear")
+    return y.reshape(*lead, n)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``rms_norm(x, weight, eps)`` of engine/model.py:29-34 as one kernel:
+    h = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))), the mean in fp32.
+    x: bf16 [..., K] on a ROCm GPU; weight: bf16 [K] on the same GPU."""
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise RuntimeError("rmsnorm: x must be on a ROCm GPU")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("rmsnorm: x and weight must be bf16")
+    k = x.shape[-1]
+    if weight.device != x.device or weight.numel() != k:
+        raise ValueError(f"rmsnorm: weight must be a bf16 [{k}] tensor on {x.device}")
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    w = weight.reshape(k).contiguous()
+    h = torch.empty_like(x2)
+    lib = _native.load()
+    with _on_device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        rc = lib.pgs_rmsnorm(_ptr(x2), _ptr(w), ctypes.c_float(eps), _ptr(h), x2.shape[0], k, ctypes.c_void_p(stream))
+    check(rc, "rmsnorm")
+    return h.reshape(x.shape)
 
 
 def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list | None = None,
@@ -369,10 +434,12 @@ def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> t
     return act.reshape(*lead, n)
 
 
-def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "QuantizedWeight") -> torch.Tensor:
-    """``F.linear(F.silu(gate(x)) * up(x), down)`` (engine/model.py:188-190, without
-    the residual add): the fused gate/up kernel, then the down projection."""
-    return linear(swiglu(x, gate, up), down)
+def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "QuantizedWeight",
+        residual: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(F.silu(gate(x)) * up(x), down)`` (engine/model.py:188-190): the
+    fused gate/up kernel, then the down projection; with ``residual`` the
+    add of engine/model.py:190 runs in the down projection's epilogue."""
+    return linear(swiglu(x, gate, up), down, residual=residual)
 
 
 # ---------------------------------------------------------------------------
@@ -435,8 +502,9 @@ class QuantizedWeight:
         return _dequantize_packed(self.qp, self.scale, *self.shape, self.dtype)
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
-               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-        return linear(x, self, bias, out_dtype=out_dtype)
+               out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+        return linear(x, self, bias, out_dtype=out_dtype, residual=residual, out=out)
 
     def _kernel_operands(self) -> tuple[torch.Tensor, torch.Tensor]:
         qp = self.qp
