@@ -108,6 +108,43 @@ def per_call_sweep(layers, x, xo, xi, m):
     return step, per_layer_b * len(layers), per_layer_f * len(layers), 7 * len(layers)
 
 
+def reference_rms_norm(x, weight, eps):
+    """engine/model.py:29-34 as the reference runs it (a chain of torch ops)."""
+    dtype = x.dtype
+    xf = x.float()
+    variance = xf.pow(2).mean(-1, keepdim=True)
+    xf = xf * torch.rsqrt(variance + eps)
+    return weight * xf.to(dtype)
+
+
+def layer_chain(layers, x0, attn, norms, fused):
+    """The decoder layers' linears with their neighbours (engine/model.py:165-190,
+    attention replaced by a fixed input): norm -> q|k|v, x += o(attn),
+    norm -> gate|up -> down, x += down.  fused: the RMSNorm kernel and the
+    residual adds in the linear epilogues; otherwise the reference's torch op
+    chain and separate adds around the same linears."""
+    from pageserve_amd import quantization as Q
+
+    def step():
+        x = x0
+        for L, (ln1, ln2) in zip(layers, norms):
+            if fused:
+                h = Q.rmsnorm(x, ln1, 1e-6)
+                Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                x = L["o"].linear(attn, residual=x)
+                h = Q.rmsnorm(x, ln2, 1e-6)
+                x = Q.mlp(h, L["gate"], L["up"], L["down"], residual=x)
+            else:
+                h = reference_rms_norm(x, ln1, 1e-6)
+                Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                x = x + L["o"].linear(attn)
+                h = reference_rms_norm(x, ln2, 1e-6)
+                x = x + Q.mlp(h, L["gate"], L["up"], L["down"])
+        return x
+
+    return step
+
+
 def capture(fn):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -365,13 +402,29 @@ def main():
             log(f"[bench] dominant kernel: {roof['launch_us']} us/launch, {roof['achieved']} GB/s")
             down_roof = kernel_roofline(layers, lambda L: L["down"].linear(xi), linear_bytes(m, HIDDEN, INTER),
                                         2 * m * HIDDEN * INTER, "hbm")
+            # the layer chain with its neighbours, fused vs the reference's structure
+            ng = torch.Generator(device=dev).manual_seed(77)
+            norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
+                           for _ in range(2)) for _ in layers]
+            chain = {}
+            for fused in (False, True):
+                cg, _ = capture(layer_chain(layers, x, xo, norms, fused))
+                chain[fused] = time_graph(cg, max(20, args.steps // 4), 5)
+                del cg
+            log(f"[bench] decode layer chain with neighbours: fused {chain[True] * 1e3 / len(layers):.2f} us/layer, "
+                f"reference structure {chain[False] * 1e3 / len(layers):.2f} us/layer")
             result.update({
                 "value": round(value, 2), "ms_per_step": round(ms, 5), "roofline": roof,
                 "decode_detail": {"frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                                   "bytes_per_step": nbytes, "launches_per_step": launches,
                                   "eager_ms_per_step": round(ms_eager, 5),
                                   "eager_gbs": round(nbytes / (ms_eager * 1e-3) / 1e9, 2),
-                                  "down_proj_roofline": down_roof},
+                                  "down_proj_roofline": down_roof,
+                                  "layer_chain_with_neighbours": {
+                                      "what": "per layer: rmsnorm, q|k|v, o + residual, rmsnorm, gate|up, down + "
+                                              "residual (attention output fixed); HIP-graph replay",
+                                      "fused_us_per_layer": round(chain[True] * 1e3 / len(layers), 3),
+                                      "reference_structure_us_per_layer": round(chain[False] * 1e3 / len(layers), 3)}},
                 "per_call_sweep": {"ms_per_step": round(pms, 5), "gbs": round(pval, 2),
                                    "frac_of_hbm_peak": round(pval / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": pbytes, "launches_per_step": plaunch},
