@@ -302,6 +302,87 @@ def read_traffic(key):
     return None
 
 
+def other_configs(layers, dev, steps):
+    """The remaining workload sizes, one compact figure each: decode sweeps at
+    M=4 and 16, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
+    and 512, the int8 lm_head [151936, 2048] at M=1, 8 and 256 (two copies
+    alternated so the 256 MB MALL cannot hold the weight), and the single
+    [4864, 896] linear at M=1 with the reference's CPU path beside it."""
+    from pageserve_amd import quantization as Q
+
+    gen = torch.Generator(device=dev).manual_seed(4242)
+
+    def act(m, k):
+        return torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+
+    out = {}
+    for m in (4, 16):
+        step, nbytes, _, _ = fused_sweep(layers, act(m, HIDDEN), act(m, HIDDEN), m)
+        g, _ = capture(step)
+        ms = time_graph(g, steps, 3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"decode_sweep_m{m}"] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        del g
+    for m in (128, 2048):
+        step, _, nflops, _ = fused_sweep(layers, act(m, HIDDEN), act(m, HIDDEN), m)
+        g, _ = capture(step)
+        ms = time_graph(g, max(5, steps // 4), 2)
+        tf = nflops / (ms * 1e-3) / 1e12
+        out[f"prefill_sweep_m{m}"] = {"ms_per_sweep": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                      "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del g
+    for m in (1, 512):
+        x = act(m, HIDDEN)
+        g, _ = capture(lambda: [Q.mlp(x, L["gate"], L["up"], L["down"]) for L in layers])
+        ms = time_graph(g, max(5, steps // 4), 2)
+        per = ms * 1e3 / len(layers)
+        nbytes = 3 * INTER * HIDDEN + 8 * INTER + 4 * HIDDEN + 2 * m * HIDDEN + 4 * m * INTER + 2 * m * HIDDEN
+        nflops = 6 * m * INTER * HIDDEN
+        out[f"swiglu_mlp_m{m}"] = {"us_per_layer": round(per, 2), "GB/s": round(nbytes / (per * 1e-6) / 1e9, 1),
+                                   "TFLOP/s": round(nflops / (per * 1e-6) / 1e12, 1)}
+        del g
+    vocab = 151936
+    heads = []
+    for c in range(2):
+        hg = torch.Generator(device=dev).manual_seed(9000 + c)
+        w = torch.randn((vocab, HIDDEN), generator=hg, device=dev) * 0.02
+        heads.append(Q.QuantizedWeight(w))
+        del w
+    torch.cuda.empty_cache()
+    for m in (1, 8, 256):
+        x = act(m, HIDDEN)
+        g, _ = capture(lambda: [hw.linear(x, out_dtype=torch.float32) for hw in heads * 4])
+        ms = time_graph(g, max(5, steps // 10), 2)
+        per = ms * 1e3 / 8
+        nbytes = vocab * HIDDEN + 4 * vocab + 2 * m * HIDDEN + 4 * m * vocab
+        out[f"lm_head_m{m}"] = {"us_per_launch": round(per, 2), "GB/s": round(nbytes / (per * 1e-6) / 1e9, 1),
+                                "TFLOP/s": round(2 * m * vocab * HIDDEN / (per * 1e-6) / 1e12, 1)}
+        del g
+    del heads
+    torch.cuda.empty_cache()
+    # the single [4864, 896] linear at M=1 (Qwen2.5-0.5B gate_proj)
+    w = torch.randn((4864, 896), generator=gen, device=dev) * 0.02
+    qw = Q.QuantizedWeight(w)
+    x = act(1, 896)
+    g, _ = capture(lambda: [qw.linear(x) for _ in range(20)])
+    us = time_graph(g, 20, 3) * 1e3 / 20
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import reference_cpu_path as R
+
+    q_cpu, s_cpu, x_cpu = qw.q.cpu(), qw.scale.cpu(), x.cpu()
+    torch.set_num_threads(R.cpu_threads())
+    R.per_call_linear(x_cpu, q_cpu, s_cpu)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        R.per_call_linear(x_cpu, q_cpu, s_cpu)
+    cpu_us = (time.perf_counter() - t0) / 20 * 1e6
+    nbytes = linear_bytes(1, 4864, 896)
+    out["single_linear_4864x896_m1"] = {"gpu_us": round(us, 2), "gpu_GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                        "cpu_reference_path_us": round(cpu_us, 1), "cpu_threads": R.cpu_threads()}
+    return out
+
+
 def cpu_baseline(layers, m, budget_s):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference_cpu_path as R
@@ -328,7 +409,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for the baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "configs"], default="all")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workload sizes")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the dispatches the rocprofv3 --pmc traffic passes read")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -446,12 +528,19 @@ def main():
             proof = kernel_roofline(layers, lambda L: Q.swiglu(px, L["gate"], L["up"]),
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
-            proof["kernel"] = "gemm_k64_kernel<BM=64,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
+            proof["kernel"] = "gemm_k64_kernel<BM=128,BN=64,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
             proof["traffic"] = read_traffic("gemm_gate_up_m512") if pm == 512 else None
             result["prefill"] = {"m": pm, "value": round(tflops, 2), "unit": "TFLOP/s",
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                                  "ms_per_step": round(ms, 5), "flops_per_step": nflops, "steps": psteps,
                                  "roofline": proof}
+
+        # ---------------- the other workload sizes ----------------
+        if args.only in ("all", "configs") and not args.no_configs:
+            oc = other_configs(layers, dev, args.steps)
+            for key, v in oc.items():
+                log(f"[bench] {key}: {v}")
+            result["other_configs"] = oc
 
         # ---------------- CPU baseline ----------------
         if not args.no_cpu_baseline and args.only in ("all", "decode"):
@@ -479,7 +568,7 @@ def main():
                    "weight_dtype": "int8", "activation_dtype": "bf16", "accumulate": "fp32",
                    "parallelism": "none (1 GPU)"},
     }
-    for key in ("roofline", "cpu_baseline", "prefill", "per_call_sweep", "decode_detail"):
+    for key in ("roofline", "cpu_baseline", "prefill", "per_call_sweep", "decode_detail", "other_configs"):
         if key in result:
             line[key] = result[key]
     print(json.dumps(line), flush=True)
