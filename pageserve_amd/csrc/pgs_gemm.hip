@@ -388,19 +388,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), 0, uniform(n), kRsrcWord3);
 }
 
-//  * KG = 2 runs two groups of four waves per workgroup on alternate K steps
-//    (each group with its own LDS stages), so a workgroup of a small tile
-//    still gives every SIMD two waves; group 1 hands its accumulators to
-//    group 0 through LDS at the end.  Both groups run the same number of
-//    iterations (a group past its last step loads its last step again and
-//    skips the MFMAs), so every barrier is reached by all waves.
+//  * KG = 2 or 4 runs that many groups of four waves per workgroup on
+//    interleaved K steps (each group with its own LDS stages), so a workgroup
+//    of a small tile still gives every SIMD KG waves and keeps KG times the
+//    weight bytes in flight; the other groups hand their accumulators to
+//    group 0 through LDS at the end, one at a time in a fixed order.  All
+//    groups run the same number of iterations (a group past its last step
+//    loads its last step again and skips the MFMAs), so every barrier is
+//    reached by all waves.
 template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG>
 __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
   constexpr int TM = BM / 16, TN = BN / 64;
   static_assert(BN % 64 == 0, "weight rows per tile: 4 waves x 16-row multiples");
   constexpr int WSETS = WLEAD + 1;               // rotating weight register sets
   constexpr int UNROLL = lcm3(WSETS, XLEAD, 2);  // static set and stage indices
-  static_assert(BM % 32 == 0 && WLEAD >= 1 && XLEAD >= 1 && (KG == 1 || KG == 2), "tile shape / pipeline");
+  static_assert(BM % 32 == 0 && WLEAD >= 1 && XLEAD >= 1 && (KG == 1 || KG == 2 || KG == 4), "tile shape / pipeline");
   constexpr int XS = BM * kBK;           // bf16 elements of one activation stage
   constexpr int XL = BM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
   constexpr int kStageBytes = KG * 2 * XS * 2;
@@ -536,24 +538,31 @@ __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint
   run_steps(step, 0, iters, std::make_integer_sequence<int, UNROLL>{});
 
   if constexpr (KG > 1) {
-    // group 1's accumulators -> LDS (the stages are free after the last barrier)
+    // groups KG-1 .. 1 hand their accumulators to group 0 through LDS, one
+    // group at a time (fixed order; the stages are free after the last barrier)
     f32x4* red = reinterpret_cast<f32x4*>(smem);
-    if (kg == 1) {
 #pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat)
+    for (int src = KG - 1; src >= 1; --src) {
+      if (kg == src) {
 #pragma unroll
-        for (int nt = 0; nt < TN; ++nt)
+        for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-          for (int mt = 0; mt < TM; ++mt) red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+          for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < TM; ++mt) red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+      }
+      __syncthreads();
+      if (kg == 0) {
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] += red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane];
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    if (kg == 1) return;
-#pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-      for (int nt = 0; nt < TN; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] += red[(((wave * NMAT + mat) * TN + nt) * TM + mt) * 64 + lane];
+    if (kg != 0) return;
   }
   if (ga.splits > 1) {
     store_partials<TN, TM, NMAT>(acc, ga, t, s, wave, lane);
@@ -664,11 +673,20 @@ int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 
 template <int NMAT, bool OUT_F32>
 int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hipStream_t st) {
-  // the SwiGLU pair at more than 64 tokens: 128 tokens x 64 rows per matrix
-  // (each widened weight operand feeds 8 MFMAs; B operands are reused across
-  // the pair's two A tiles per wave)
-  if constexpr (NMAT == 2)
-    if (plan.bm == 128) return launch_k64<128, 64, 2, OUT_F32, 2, 1, 2>(x, ga, st);
+  if (ga.K % kBK == 0 && plan.bn == 64) {
+    if constexpr (NMAT == 2) {
+      // the SwiGLU pair above 128 tokens: 128 tokens x 64 rows per matrix
+      // (each widened weight operand feeds 8 MFMAs; B operands are reused
+      // across the pair's two A tiles per wave); 17..128 tokens: 64 x 64
+      // tiles in two K groups
+      if (plan.bm == 128) return launch_k64<128, 64, 2, OUT_F32, 2, 1, 2>(x, ga, st);
+      return launch_k64<64, 64, 2, OUT_F32, 2, 2, 1, 2>(x, ga, st);
+    } else {
+      // single matrices at 17..128 tokens: 64-row tiles in four K groups
+      return plan.bm == 32 ? launch_k64<32, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st)
+                           : launch_k64<64, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
+    }
+  }
   return plan.bm == 32 ? launch_bm<32, NMAT, OUT_F32>(x, ga, st) : launch_bm<64, NMAT, OUT_F32>(x, ga, st);
 }
 
@@ -676,11 +694,29 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
 
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split) {
   GemmPlan p{};
-  p.bn = (nmat == 2 && m > 64 && k % kBK == 0) ? 64 : kBN;
+  const int kb = (k + kBK - 1) / kBK;
+  // 17..128 tokens (K % 64 == 0): weight streaming dominates, so 64-row
+  // tiles and K groups keep more workgroups and more weight bytes in flight
+  const bool mid = k % kBK == 0 && m <= 128;
+  p.bn = (mid || (nmat == 2 && k % kBK == 0)) ? 64 : kBN;
+  p.kg = 1;
   int tiles_n = 0;
   for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
-  const int kb = (k + kBK - 1) / kBK;
   auto tiles_for = [&](int bm) { return static_cast<int64_t>((m + bm - 1) / bm) * tiles_n; };
+  if (mid) {
+    p.bm = (nmat == 1 && kb <= 64) ? 32 : 64;
+    p.kg = nmat == 2 ? 2 : 4;
+    p.tiles_m = (m + p.bm - 1) / p.bm;
+    p.tiles_n = tiles_n;
+    p.tiles = p.tiles_m * p.tiles_n;
+    p.splits = 1;
+    // long K (down_proj): split K until about four 16-wave workgroups per CU
+    if (can_split && nmat == 1 && kb > 64) {
+      while (p.splits < 4 && static_cast<int64_t>(p.tiles) * p.splits * p.kg < 1024 && kb / (p.splits * 2) >= 8 * p.kg)
+        p.splits *= 2;
+    }
+    return p;
+  }
   p.bm = p.bn == 64 ? 128 : m <= 32 ? 32 : 64;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K

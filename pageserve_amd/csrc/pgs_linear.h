@@ -51,6 +51,7 @@ struct SkinnyPlan {
 // Launch plan of the tile GEMM (m > 16).
 struct GemmPlan {
   int bm, bn;     // output tile (tokens x weight rows)
+  int kg;         // K groups of four waves per workgroup (K % 64 == 0 kernel)
   int tiles_m, tiles_n, tiles;
   int splits;     // workgroups per output tile along K
 };

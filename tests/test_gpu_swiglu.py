@@ -31,7 +31,8 @@ def _mlp_weights(gpu, seed, inter, hidden):
                                             (3, 100, 48), (40, 300, 208), (20, 64, 16),
                                             (50, 130, 48), (24, 256, 4112),
                                             # 128-token x 64-row tiles: split K, ragged M and N
-                                            (100, 256, 4096), (300, 1000, 2048), (65, 64, 64)])
+                                            (100, 256, 4096), (300, 1000, 2048), (65, 64, 64),
+                                            (33, 1000, 2048)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
     ws = _mlp_weights(gpu, 10 + m + inter, inter, hidden)
     x = activations(m, m, hidden)
