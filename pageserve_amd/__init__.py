@@ -11,9 +11,11 @@ from .quantization import (  # noqa: F401
     dequantize,
     linear,
     linear_group,
+    load_quantized,
     mlp,
     quantize_per_channel,
     rmsnorm,
+    save_quantized,
     swiglu,
 )
 

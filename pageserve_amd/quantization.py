@@ -48,6 +48,9 @@ __all__ = [
     "swiglu",
     "mlp",
     "rmsnorm",
+    "save_quantized",
+    "load_quantized",
+    "packed_numel",
     "pack",
     "unpack",
 ]
@@ -506,6 +509,39 @@ class QuantizedWeight:
                out: torch.Tensor | None = None) -> torch.Tensor:
         return linear(x, self, bias, out_dtype=out_dtype, residual=residual, out=out)
 
+    # -- persistent form (the reference re-quantizes at every load,
+    # engine/model.py:101-112; the stored packed form loads as a copy) --
+
+    def state(self) -> dict[str, torch.Tensor]:
+        """The stored form: packed int8 ``qp``, fp32 ``scale`` [N, 1] and
+        ``meta`` = int64 [N, K, dtype code] (0 fp32, 1 bf16, 2 fp16)."""
+        code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}.get(self.dtype)
+        if code is None:
+            raise TypeError(f"cannot store a QuantizedWeight of dtype {self.dtype}")
+        return {"qp": self.qp, "scale": self.scale,
+                "meta": torch.tensor([self.shape[0], self.shape[1], code], dtype=torch.int64)}
+
+    @classmethod
+    def from_state(cls, state: dict[str, torch.Tensor]) -> "QuantizedWeight":
+        """Rebuilds a QuantizedWeight from :meth:`state` (no quantization, no
+        kernel launch); the tensors stay on their device."""
+        try:
+            qp, scale, meta = state["qp"], state["scale"], state["meta"]
+        except KeyError as e:
+            raise ValueError(f"QuantizedWeight state lacks {e}") from None
+        n, k, code = (int(v) for v in meta.reshape(-1).tolist())
+        dtype = {0: torch.float32, 1: torch.bfloat16, 2: torch.float16}.get(code)
+        if dtype is None or n < 0 or k < 0:
+            raise ValueError(f"bad QuantizedWeight meta {meta.tolist()}")
+        if qp.dtype != torch.int8 or qp.numel() != packed_numel(n, k):
+            raise ValueError(f"packed weight must be int8 with {packed_numel(n, k)} elements for [{n}, {k}]")
+        if scale.dtype != torch.float32 or scale.numel() != n or scale.device != qp.device:
+            raise ValueError(f"scale must be fp32 [{n}, 1] on {qp.device}")
+        obj = cls.__new__(cls)
+        obj.dtype, obj.shape = dtype, torch.Size((n, k))
+        obj.qp, obj.scale = qp.reshape(-1), scale.reshape(n, 1)
+        return obj
+
     def _kernel_operands(self) -> tuple[torch.Tensor, torch.Tensor]:
         qp = self.qp
         if not qp.is_contiguous() or (qp.numel() and qp.data_ptr() % 16):
@@ -514,6 +550,42 @@ class QuantizedWeight:
         if s.dtype != torch.float32 or not s.is_contiguous():
             s = s.to(torch.float32).contiguous()
         return qp, s
+
+
+def packed_numel(n: int, k: int) -> int:
+    """Bytes of the packed tile layout of an [n, k] int8 matrix (16-row x
+    64-column blocks of 1 KiB, zero padded)."""
+    return ((n + 15) // 16) * ((k + 63) // 64) * 1024 if n > 0 and k > 0 else 0
+
+
+_FORMAT = "pageserve_amd.w8a16.packed.v1"
+
+
+def save_quantized(path: str, weights: dict[str, "QuantizedWeight"]) -> None:
+    """Writes quantized weights to a safetensors file (tensors ``<name>.qp``,
+    ``<name>.scale``, ``<name>.meta``); executes nothing when loaded."""
+    from safetensors.torch import save_file
+
+    tensors = {}
+    for name, w in weights.items():
+        for key, t in w.state().items():
+            tensors[f"{name}.{key}"] = t.detach().to("cpu").contiguous()
+    save_file(tensors, path, metadata={"format": _FORMAT})
+
+
+def load_quantized(path: str, device: str | torch.device = "cpu") -> dict[str, "QuantizedWeight"]:
+    """Reads :func:`save_quantized` output onto ``device`` (a copy: no
+    quantization at load)."""
+    from safetensors import safe_open
+
+    out: dict[str, dict[str, torch.Tensor]] = {}
+    with safe_open(path, framework="pt", device=str(device)) as f:
+        if (f.metadata() or {}).get("format") != _FORMAT:
+            raise ValueError(f"{path}: not a pageserve_amd quantized-weight file")
+        for key in f.keys():
+            name, _, field = key.rpartition(".")
+            out.setdefault(name, {})[field] = f.get_tensor(key)
+    return {name: QuantizedWeight.from_state(st) for name, st in out.items()}
 
 
 class W8A16Weight(torch.Tensor):
