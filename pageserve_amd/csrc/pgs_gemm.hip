@@ -342,7 +342,6 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(const uint16_t* __r
 //  * Weights run two K steps ahead in three rotating register sets,
 //    activations XLEAD steps ahead through double-buffered LDS; the loop is
 //    unrolled by six so every set and stage index is static.
-constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 
 // Runs step(integral_constant<i>, kt) for kt = kt0 .. kt1-1 with the loop
 // body unrolled over i = 0 .. sizeof...(Is)-1; the fold stops after the step
@@ -371,21 +370,6 @@ __device__ __forceinline__ void block_order(int t, int tiles_n, int tiles_m, int
   const int rem = r - mb * gn_size * kGroup;
   tn = gn * kGroup + rem / gm_size;
   tm = mb * kGroup + rem % gm_size;
-}
-
-// A buffer resource must live in scalar registers; values the compiler cannot
-// prove wave-uniform (pointers picked from the argument arrays) are moved
-// there explicitly.  The inputs are uniform by construction.
-__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ const void* uniform(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);  // integer clamp (no fp round trip)
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), 0, uniform(n), kRsrcWord3);
 }
 
 //  * KG = 2 or 4 runs that many groups of four waves per workgroup on

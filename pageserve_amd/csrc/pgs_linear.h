@@ -35,6 +35,10 @@ struct Problem {
   unsigned long long* pairs;  // zeroed pair slots (skinny two-way split), or null
 };
 
+// Largest in_features of the linear kernels: their buffer offsets
+// (row * K * 2 bytes for up to 128 activation rows) are 32-bit.
+constexpr int kMaxK = 1 << 22;
+
 // Workspace layout: kPairBytes of pair slots (zero before first use, left
 // zero by every call), then the split-K partial tiles.  One 8-byte slot per
 // output of a 16-row tile: 256 tiles x 16 rows x 16 tokens.
@@ -43,9 +47,9 @@ constexpr size_t kPairBytes = 256u * 256u * 8u;
 // Launch plan of the skinny kernel (m <= 16).
 struct SkinnyPlan {
   int tiles;   // 16-row tiles over all members
-  int nw;      // waves per workgroup (split the workgroup's K range)
   int splits;  // workgroups per tile (split K across workgroups)
   bool pair;   // two K halves combined through pair slots (no reduce launch)
+  int shape;   // launch shape: waves per workgroup and chunks per wave
 };
 
 // Launch plan of the tile GEMM (m > 16).
@@ -78,11 +82,67 @@ __device__ __forceinline__ T pick(const T (&arr)[L], int g) {
   return v;
 }
 
+// The same choice with every element read into a scalar register first, so
+// the choice is a register select.  The compiler otherwise folds the selects
+// into one load from a computed kernel-argument offset, which puts a second,
+// dependent scalar memory round trip in front of the kernel's first vector
+// load: worth avoiding in short (decode) kernels, whose run time is mostly
+// such latencies.  Pointers pass the barrier as global-memory pointers, so
+// accesses through the result stay global (not flat) loads and stores.
+template <typename T, int L>
+__device__ __forceinline__ T pick_early(const T (&arr)[L], int g) {
+  T v[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    v[i] = arr[i];
+    asm volatile("" : "+s"(v[i]));
+  }
+  T r = v[0];
+#pragma unroll
+  for (int i = 1; i < L; ++i) r = (g == i) ? v[i] : r;
+  return r;
+}
+template <typename T, int L>
+__device__ __forceinline__ T* pick_early(T* const (&arr)[L], int g) {
+  using GT = __attribute__((address_space(1))) T;
+  GT* v[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    v[i] = (GT*)arr[i];
+    asm volatile("" : "+s"(v[i]));
+  }
+  GT* r = v[0];
+#pragma unroll
+  for (int i = 1; i < L; ++i) r = (g == i) ? v[i] : r;
+  return (T*)r;
+}
+
 __device__ __forceinline__ int member_of(const GroupArgs& a, int unit) {
   int g = 0;
 #pragma unroll
   for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (i < a.n_outs && unit >= a.unit_begin[i]) ? i : g;
   return g;
+}
+
+// Buffer loads: a resource (base, byte size) in scalar registers, a
+// per-lane offset and a wave-uniform offset; the hardware range check
+// returns zeros for bytes past the size, without a memory access.
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int kLoadNT = 2;              // cache policy: non-temporal (streamed once)
+
+// A buffer resource must live in scalar registers; values the compiler cannot
+// prove wave-uniform (pointers picked from the argument arrays) are moved
+// there explicitly.  The inputs are uniform by construction.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const void* uniform(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);  // integer clamp (no fp round trip)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), 0, uniform(n), kRsrcWord3);
 }
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

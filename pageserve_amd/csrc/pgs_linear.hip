@@ -73,7 +73,9 @@ int run(Problem& p, void* workspace, size_t ws_bytes, hipStream_t st) {
 int check_common(const char* fn, const void* x, int64_t m, int64_t k) {
   if (m < 0 || k < 0)
     return fail(PGS_ERR_INVALID_ARGUMENT, "%s: negative size m=%lld k=%lld", fn, (long long)m, (long long)k);
-  if (m > 0x7fffffff || k > 0x7fffffff) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: size too large", fn);
+  if (m > 0x7fffffff) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: size too large", fn);
+  // (32-bit buffer offsets inside the kernels)
+  if (k > kMaxK) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: in_features k=%lld above %d", fn, (long long)k, kMaxK);
   if (k % 16 != 0)
     return fail(PGS_ERR_INVALID_ARGUMENT, "%s: in_features k=%lld must be a multiple of 16", fn, (long long)k);
   if (m > 0 && k > 0 && !x) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null activation pointer", fn);

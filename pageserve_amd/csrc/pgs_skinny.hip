@@ -9,15 +9,14 @@
 //
 // Work decomposition: one workgroup per (16-row tile, K split).  The NW waves
 // of a workgroup take 64-k chunks of its K range round robin, U chunks per
-// batch with every load of a batch in flight together, and their partial
-// 16x16 tiles are summed through LDS in a fixed order.  Short-N shapes
-// (o_proj, down_proj: 128 tiles) would leave half of the 256 CUs idle, so
-// their K range is split over several workgroups: each writes its partial
-// tile to the workspace and a second small kernel sums the partials in split
-// order and runs the epilogue.  (Combining them inside one kernel would need
-// an agent-scope release per workgroup, which writes back the whole L2 and
-// costs far more than the extra launch.)  Results never depend on timing:
-// every sum has a fixed order.
+// batch; for the K ranges of the usual shapes a wave issues all of its
+// batches at once, so a short launch costs one memory round trip rather than
+// one per batch.  The waves' partial 16x16 tiles are summed through LDS in a
+// fixed order.  Short-N shapes (o_proj, down_proj: 128 tiles) would leave
+// half of the 256 CUs idle, so their K range may be split over two
+// workgroups that meet in a pair slot (below); the SwiGLU pair splits
+// through workspace partials and a second small kernel instead.  Results
+// never depend on timing: every sum has a fixed order.
 #include "pgs_linear.h"
 
 namespace pgs {
@@ -27,49 +26,103 @@ namespace {
 // (i/4)*16 + mm, register i%4
 __device__ __forceinline__ int acc_lane(int i, int mm) { return (i >> 2) * 16 + mm; }
 
+// Operands of one output's epilogue (scales, bias, residual), loaded before
+// the weight stream so that their memory round trip overlaps it instead of
+// following it.  The loads are unconditional (an absent bias or residual
+// reads a valid dummy address instead and is ignored), so no branch makes
+// the kernel wait for them before the weight loads are issued; the bf16
+// values stay raw until the epilogue.
+template <int NMAT>
+struct EpiIn {
+  float s[NMAT];
+  uint16_t bias, res;
+};
+
+template <int NMAT>
+__device__ __forceinline__ EpiIn<NMAT> epilogue_load(const GroupArgs& a, int g, int n, int mm, int N,
+                                                     const uint16_t* dummy) {
+  EpiIn<NMAT> e;
+  if constexpr (NMAT == 2) {
+    e.s[0] = a.scale[0][n];
+    e.s[1] = a.scale[1][n];
+    e.bias = e.res = 0;
+  } else {
+    const float* sc = pick_early(a.scale, g);
+    const uint16_t* bias = pick_early(a.bias, g);
+    const uint16_t* res = pick_early(a.res, g);
+    e.s[0] = sc[n];
+    e.bias = *(bias ? bias + n : dummy);
+    e.res = *(res ? res + static_cast<int64_t>(mm) * N + n : dummy);
+  }
+  return e;
+}
+
 template <int NMAT, bool OUT_F32>
-__device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int mm, int N, const float (&v)[NMAT]) {
-  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
-  void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
+__device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int mm, int N, const float (&v)[NMAT],
+                                         const EpiIn<NMAT>& e) {
+  void* y = (NMAT == 2) ? a.y[0] : pick_early(a.y, g);
   float out;
   if constexpr (NMAT == 2) {
-    out = silu_f32(v[0] * sc0[n]) * (v[1] * a.scale[1][n]);
+    out = silu_f32(v[0] * e.s[0]) * (v[1] * e.s[1]);
   } else {
-    out = v[0] * sc0[n];
-    const uint16_t* bias = pick(a.bias, g);
-    if (bias) out += bf16_bits_to_f32(bias[n]);
-    out = add_residual<OUT_F32>(out, pick(a.res, g), static_cast<int64_t>(mm) * N + n);
+    out = v[0] * e.s[0];
+    if (pick_early(a.bias, g)) out += bf16_bits_to_f32(e.bias);
+    if (pick_early(a.res, g)) {
+      // the reference's roundings (engine/model.py:184, 190): the linear
+      // output is rounded to the output type first, then added
+      const float l = OUT_F32 ? out : bf16_bits_to_f32(f32_to_bf16_bits(out));
+      out = l + bf16_bits_to_f32(e.res);
+    }
   }
   store_out<OUT_F32>(y, static_cast<int64_t>(mm) * N + n, out);
 }
 
-template <int NW, int U, int NMAT, bool OUT_F32, bool K64>
-__global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
+// Waves per SIMD the compiler must leave room for: the SwiGLU pair at
+// 8 waves x 2 batches holds 64 registers of loads per lane, and three of its
+// workgroups per CU (all 688 of a 2048 x 11008 pair resident at once) need
+// <= 80 registers.
+constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
+
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64>
+__global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int tile = blockIdx.x / splits;
   const int s = blockIdx.x - tile * splits;
 
   const int g = (NMAT == 2) ? 0 : member_of(a, tile);
-  const int N = pick(a.n, g);
-  const int row0 = (tile - pick(a.unit_begin, g)) * 16;
+  const int N = pick_early(a.n, g);
+  const int row0 = (tile - pick_early(a.unit_begin, g)) * 16;
   const int lrow = lane & 15;
   const int kgrp = lane >> 4;
 
-  // packed weights: block (tile, chunk) is 1 KiB, this lane's 16 bytes at lane*16
+  // one output per thread (M * 16 <= 256 <= 64 * NW)
+  static_assert(NW >= 4, "the epilogue gives each thread at most one output");
+  const int idx = threadIdx.x;
+  const int mm = idx >> 4, oi = idx & 15;
+  const bool has_out = idx < M * 16 && row0 + oi < N;
+
+  // (splits <= 2 and nchunks <= 2^16: 32-bit arithmetic)
   const int nchunks = (K + 63) >> 6;
-  const int8_t* wrow[NMAT];
+  const int cb = s * nchunks / splits;
+  const int ce = (s + 1) * nchunks / splits;
+  // Packed weights: block (tile, chunk) is 1 KiB, this lane's 16 bytes at
+  // lane * 16.  One buffer resource per matrix spans exactly this
+  // workgroup's chunks [cb, ce) of its 16-row block row, so a chunk past the
+  // range reads zeros without touching memory.
+  __amdgpu_buffer_rsrc_t wres[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
-    const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick(a.q, g);
-    wrow[mat] = qg + static_cast<int64_t>(row0 >> 4) * nchunks * 1024 + lane * 16;
+    const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick_early(a.q, g);
+    wres[mat] = make_rsrc(qg + (static_cast<int64_t>(row0 >> 4) * nchunks + cb) * 1024,
+                          static_cast<int64_t>(ce - cb) * 1024);
   }
-  const uint16_t* xrow = x + static_cast<int64_t>(min(lrow, M - 1)) * K + kgrp * 16;
-
-  const int cb = static_cast<int>(static_cast<int64_t>(s) * nchunks / splits);
-  const int ce = static_cast<int>(static_cast<int64_t>(s + 1) * nchunks / splits);
+  const int woff = lane * 16;
+  // activations: row min(lrow, M - 1), this lane's 16 columns of each chunk
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<int64_t>(M) * K * 2);
+  const int xoff = min(lrow, M - 1) * K * 2 + kgrp * 32;
 
   f32x4 acc[NMAT];
 #pragma unroll
@@ -85,9 +138,17 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
     }
   };
 
-  // Full batches of U chunks, software pipelined: the loads of the next batch
-  // are issued before the MFMAs of the current one, so every wave keeps a
-  // batch in flight while it computes.
+  // Batches of U chunks: batch j of this wave covers chunks c(j) .. c(j)+U-1,
+  // c(j) = cb + (j * NW + wave) * U.  Every load is issued and every MFMA
+  // run unconditionally, in a fixed order (a chunk at or past ce reads zero
+  // weights, and its activations are masked to zero as well, so that
+  // non-finite inputs of other K ranges cannot leak in); with no branch the
+  // compiler can neither sink a load towards its use nor lose count: its
+  // wait before each batch's MFMAs counts exactly the loads issued after it,
+  // and nothing waits for more than its own data.  The loads carry no address
+  // arithmetic: K advances in the scalar offset.  NB > 0: the wave's NB
+  // batches are all issued up front (one memory round trip for the whole
+  // workgroup); NB = 0 (long K): groups of two batches in a loop.
   struct Batch {
     u32x4 w[U][NMAT];
     u32x4 x[U][2];
@@ -95,51 +156,46 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
   auto load_batch = [&](Batch& b, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int koff = (c + u) * 64;
-      // activations are not padded: a chunk past K reloads the first 16
-      // columns of the row (in bounds, K >= 16) and mac_batch zeroes it
-      // (branch free; masking here would wait at issue)
-      const int xo = (K64 || koff + kgrp * 16 < K) ? koff : -kgrp * 16;
+      const int cc = c + u;
 #pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) b.w[u][mat] = ld16_stream(wrow[mat] + (c + u) * 1024);
-      b.x[u][0] = ld16(xrow + xo);
-      b.x[u][1] = ld16(xrow + xo + 8);
+      for (int mat = 0; mat < NMAT; ++mat)
+        b.w[u][mat] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff, (cc - cb) * 1024, kLoadNT);
+      // (K % 64 != 0: columns past K read the next row or zeros; mac_batch
+      // masks them)
+      b.x[u][0] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, cc * 128, 0);
+      b.x[u][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, cc * 128, 0);
     }
   };
   auto mac_batch = [&](const Batch& b, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t mask = (K64 || (c + u) * 64 + kgrp * 16 < K) ? 0xffffffffu : 0u;
+      const bool on = c + u < ce && (K64 || (c + u) * 64 + kgrp * 16 < K);
+      const uint32_t mask = on ? 0xffffffffu : 0u;
       mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
     }
   };
   constexpr int kStep = NW * U;
-  int c0 = cb + wave * U;
-  if (c0 + U <= ce) {
-    Batch cur;
-    load_batch(cur, c0);
-    while (c0 + kStep + U <= ce) {
-      Batch nxt;
-      load_batch(nxt, c0 + kStep);
-      mac_batch(cur, c0);
-      cur = nxt;
-      c0 += kStep;
-    }
-    mac_batch(cur, c0);
-    c0 += kStep;
-  }
-  // the last partial batch of this wave, one chunk at a time
-  for (int c = c0; c < min(c0 + U, ce); ++c) {
-    const int koff = c * 64;
-    const bool on = K64 || koff + kgrp * 16 < K;
-    u32x4 wv[NMAT];
+  const int first = cb + wave * U;
+  // epilogue operands (clamped to a valid output, so the loads need no branch)
+  auto load_epi = [&] { return epilogue_load<NMAT>(a, g, min(row0 + oi, N - 1), min(mm, M - 1), N, x); };
+  EpiIn<NMAT> epi;
+  if constexpr (NB > 0) {
+    Batch bt[NB];
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) wv[mat] = ld16_stream(wrow[mat] + c * 1024);
-    const uint32_t mask = on ? 0xffffffffu : 0u;
-    const int xo = on ? koff : -kgrp * 16;
-    const u32x4 x0 = ld16(xrow + xo) & mask;
-    const u32x4 x1 = ld16(xrow + xo + 8) & mask;
-    mac(wv, x0, x1);
+    for (int j = 0; j < NB; ++j) load_batch(bt[j], first + j * kStep);
+    epi = load_epi();  // behind the weight loads
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+#pragma unroll
+    for (int j = 0; j < NB; ++j) mac_batch(bt[j], first + j * kStep);
+  } else {
+    epi = load_epi();
+    for (int c = first; c < ce; c += 2 * kStep) {
+      Batch b0, b1;
+      load_batch(b0, c);
+      load_batch(b1, c + kStep);
+      mac_batch(b0, c);
+      mac_batch(b1, c + kStep);
+    }
   }
 
   __shared__ f32x4 red[NW][NMAT][64];
@@ -147,41 +203,38 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint16_t* __restr
   for (int mat = 0; mat < NMAT; ++mat) red[wave][mat][lane] = acc[mat];
   __syncthreads();
 
-  const int outs = M * 16;
-  float* mine = partials + (static_cast<int64_t>(tile) * splits + s) * (NMAT * 256);
-  for (int idx = threadIdx.x; idx < outs; idx += 64 * NW) {
-    const int mm = idx >> 4, i = idx & 15;
-    const int ln = acc_lane(i, mm), r = i & 3;
-    float v[NMAT];
+  if (idx >= M * 16) return;
+  const int ln = acc_lane(oi, mm), r = oi & 3;
+  float v[NMAT];
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) {
-      float t = 0.f;
+  for (int mat = 0; mat < NMAT; ++mat) {
+    float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) t += red[w][mat][ln][r];
-      v[mat] = t;
+    for (int w = 0; w < NW; ++w) t += red[w][mat][ln][r];
+    v[mat] = t;
+  }
+  if (NMAT == 1 && pairs) {
+    // The two K halves of this tile meet in one 64-bit slot per output.
+    // The first to arrive leaves (1, its partial); the second takes it,
+    // empties the slot for the next call and finishes the output.  The data
+    // travels inside the atomic, so no fence or wait is needed, and the sum
+    // does not depend on the arrival order (fp32 addition is commutative).
+    // System scope: the two workgroups run on different XCDs, and the
+    // exchange is then performed beyond their L2s.
+    unsigned long long* slot = pairs + static_cast<int64_t>(tile) * 256 + idx;
+    const unsigned long long prev = __hip_atomic_exchange(slot, (1ull << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_SYSTEM);
+    if (prev >> 32) {
+      __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      v[0] += __uint_as_float(static_cast<uint32_t>(prev));
+      if (has_out) epilogue<NMAT, OUT_F32>(a, g, row0 + oi, mm, N, v, epi);
     }
-    if (NMAT == 1 && pairs) {
-      // The two K halves of this tile meet in one 64-bit slot per output.
-      // The first to arrive leaves (1, its partial); the second takes it,
-      // empties the slot for the next call and finishes the output.  The data
-      // travels inside the atomic, so no fence or wait is needed, and the sum
-      // does not depend on the arrival order (fp32 addition is commutative).
-      // System scope: the two workgroups run on different XCDs, and the
-      // exchange is then performed beyond their L2s.
-      unsigned long long* slot = pairs + static_cast<int64_t>(tile) * 256 + idx;
-      const unsigned long long prev = __hip_atomic_exchange(slot, (1ull << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_SYSTEM);
-      if (prev >> 32) {
-        __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        v[0] += __uint_as_float(static_cast<uint32_t>(prev));
-        if (row0 + i < N) epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v);
-      }
-    } else if (splits > 1) {
+  } else if (splits > 1) {
+    float* mine = partials + (static_cast<int64_t>(tile) * splits + s) * (NMAT * 256);
 #pragma unroll
-      for (int mat = 0; mat < NMAT; ++mat) mine[mat * 256 + idx] = v[mat];
-    } else if (row0 + i < N) {
-      epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v);
-    }
+    for (int mat = 0; mat < NMAT; ++mat) mine[mat * 256 + idx] = v[mat];
+  } else if (has_out) {
+    epilogue<NMAT, OUT_F32>(a, g, row0 + oi, mm, N, v, epi);
   }
 }
 
@@ -192,8 +245,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
                                                             const float* __restrict__ partials) {
   const int tile = blockIdx.x;
   const int g = (NMAT == 2) ? 0 : member_of(a, tile);
-  const int N = pick(a.n, g);
-  const int row0 = (tile - pick(a.unit_begin, g)) * 16;
+  const int N = pick_early(a.n, g);
+  const int row0 = (tile - pick_early(a.unit_begin, g)) * 16;
   const int idx = threadIdx.x;
   if (idx >= M * 16) return;
   const int mm = idx >> 4, i = idx & 15;
@@ -206,18 +259,23 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
     for (int sp = 0; sp < splits; ++sp) t += base[sp * (NMAT * 256) + mat * 256 + idx];
     v[mat] = t;
   }
-  epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v);
+  epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v, epilogue_load<NMAT>(a, g, row0 + i, mm, N,
+                                       reinterpret_cast<const uint16_t*>(pick_early(a.scale, g) + row0 + i)));
 }
 
-template <int NW, int U, int NMAT, bool OUT_F32>
+template <int NW, int U, int NB, int NMAT, bool OUT_F32>
 int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * plan.splits;
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
+  // NB > 0: the waves' batches must cover a workgroup's whole K range
+  const int per_wg = ((p.k + 63) / 64 + plan.splits - 1) / plan.splits;
+  if (NB > 0 && NB * U * NW < per_wg)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: plan covers %d of %d chunks", NB * U * NW, per_wg);
   if (p.k % 64 == 0)
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NMAT, OUT_F32, true>), dim3(static_cast<unsigned>(grid)), dim3(64 * NW),
-                       0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
+    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true>), dim3(static_cast<unsigned>(grid)),
+                       dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
   else
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NMAT, OUT_F32, false>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
   int rc = check_launch("w8a16 skinny kernel");
   if (rc || plan.splits == 1 || plan.pair) return rc;
@@ -226,28 +284,45 @@ int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   return check_launch("w8a16 skinny reduce kernel");
 }
 
+// Launch shapes (waves per workgroup, chunks per batch, batches per wave);
+// a workgroup covers NW * U * NB chunks of 64 k.  Index kLoopShape: the
+// looping kernel for longer ranges.
+struct SkinnyShape {
+  int nw, u, nb;
+};
+constexpr SkinnyShape kSkinnyShapes[] = {{4, 2, 1}, {4, 2, 2}, {8, 2, 2}, {16, 2, 2}, {16, 1, 6}, {16, 2, 4}, {16, 2, 0}};
+constexpr int kLoopShape = 6;
+
 template <int NMAT, bool OUT_F32>
-int launch_nw(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
-  switch (plan.nw) {
-    case 4: return launch_cfg<4, 2, NMAT, OUT_F32>(p, plan, st);
-    case 8: return launch_cfg<8, 2, NMAT, OUT_F32>(p, plan, st);
-    default: return launch_cfg<16, 2, NMAT, OUT_F32>(p, plan, st);
+int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
+  switch (plan.shape) {
+    case 0: return launch_cfg<4, 2, 1, NMAT, OUT_F32>(p, plan, st);
+    case 1: return launch_cfg<4, 2, 2, NMAT, OUT_F32>(p, plan, st);
+    case 2: return launch_cfg<8, 2, 2, NMAT, OUT_F32>(p, plan, st);
+    case 3: return launch_cfg<16, 2, 2, NMAT, OUT_F32>(p, plan, st);
+    case 4: return launch_cfg<16, 1, 6, NMAT, OUT_F32>(p, plan, st);
+    case 5:
+      if constexpr (NMAT == 1) return launch_cfg<16, 2, 4, NMAT, OUT_F32>(p, plan, st);
+      [[fallthrough]];
+    default: return launch_cfg<16, 2, 0, NMAT, OUT_F32>(p, plan, st);
   }
 }
 
 }  // namespace
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
-  (void)m;
-  (void)nmat;
   // Measured on MI355X inside HIP graphs (decode shapes of a 2048-hidden
-  // model): 8 waves per workgroup with 2-chunk pipelined batches is best for
-  // K = 2048; a long K (down_proj, K = 11008) over few tiles wants 16 waves
-  // and a 2-way K split so that twice as many CUs stream it.
-  SkinnyPlan p{tiles, 8, 1, false};
+  // model).  Every load of a workgroup is issued at once when its range fits
+  // one of the fixed shapes; fewer than 256 row tiles leave CUs idle, so a
+  // single matrix then splits K over two workgroups when K is long (down_proj:
+  // 7.1 vs 8.9 us) or when at most 128 tiles meet several tokens (o_proj at
+  // 16 tokens: 4.3 vs 4.8 us).  Otherwise a 32-chunk K is faster unsplit,
+  // without the pair slot's round trip (q|k|v, 160 tiles: 3.7 vs 4.2 us at
+  // one token, 4.9 vs 5.4 us at 16).
+  SkinnyPlan p{tiles, 1, false, kLoopShape};
   const int chunks = (k + 63) / 64;
   if (can_split && tiles < 256) {
-    if (nmat == 1 && chunks >= 16) {
+    if (nmat == 1 && chunks >= 16 && (chunks >= 64 || (m > 4 && tiles <= 128))) {
       p.splits = 2;  // K halves combined through pair slots
       p.pair = true;
     } else if (chunks >= 128) {
@@ -255,7 +330,12 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
     }
   }
   const int per_wg = (chunks + p.splits - 1) / p.splits;
-  p.nw = per_wg >= 64 ? 16 : per_wg >= 16 ? 8 : 4;
+  // (the SwiGLU pair stops at 96 chunks: 128 would not fit its registers)
+  const int last = nmat == 2 ? 4 : 5;
+  for (int i = last; i >= 0; --i) {
+    const SkinnyShape& sh = kSkinnyShapes[i];
+    if (sh.nw * sh.u * sh.nb >= per_wg) p.shape = i;
+  }
   return p;
 }
 
@@ -268,8 +348,8 @@ int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: paired split without pair slots");
   if (plan.splits > 1 && !plan.pair && (!p.partials || p.partial_bytes < skinny_partial_bytes(plan, p.nmat)))
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: split-K plan without a large enough workspace");
-  if (p.nmat == 2) return launch_nw<2, false>(p, plan, st);
-  return p.out_f32 ? launch_nw<1, true>(p, plan, st) : launch_nw<1, false>(p, plan, st);
+  if (p.nmat == 2) return launch_shape<2, false>(p, plan, st);
+  return p.out_f32 ? launch_shape<1, true>(p, plan, st) : launch_shape<1, false>(p, plan, st);
 }
 
 }  // namespace pgs
