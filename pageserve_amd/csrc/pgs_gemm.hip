@@ -44,8 +44,13 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
   return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
-// element offset (bf16 units) of 16-byte chunk `ch` of row `row` in a [rows][64] stage
-__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ ((row >> 1) & 7)) << 3); }
+// Element offset (bf16 units) of 16-byte chunk `ch` of row `row` in a
+// [rows][64] stage.  The chunk is XOR-swizzled with bits 0..2 of the row and
+// bit 3 folded into bit 0, so that the 16 lanes a 128-bit LDS access serves
+// per cycle (16 consecutive rows, one chunk column: the B-operand reads; or
+// two rows' eight chunks: the stores) hit 16 distinct 16-byte bank groups of
+// gfx950's 64 banks (measured: zero bank-conflict cycles).
+__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ (row & 7) ^ ((row >> 3) & 1)) << 3); }
 
 struct GemmArgs {
   GroupArgs g;
@@ -395,7 +400,11 @@ __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint
 
   const GroupArgs& a = ga.g;
   const int M = ga.M, K = ga.K;
-  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kg = tid >> 8;
+  // (kg is wave-uniform; readfirstlane makes that visible to the compiler, so
+  // the K offsets derived from it stay in scalar registers: a buffer load
+  // whose scalar offset sits in a vector register is wrapped in a loop over
+  // its distinct values)
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kg = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int tid_g = tid & (kThreads - 1);
   uint16_t* const xs = reinterpret_cast<uint16_t*>(smem) + kg * 2 * XS;
   // Work units: (weight tile, K split, token tile).  (split, weight tile)
@@ -476,23 +485,29 @@ __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint
 #pragma unroll
       for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Per K half: every B fragment of the half is read before its MFMAs (all
+  // TM reads in flight at once; the compiler otherwise reuses one register
+  // and waits out the LDS latency before every MFMA pair), then the weights
+  // are widened and the MFMAs issued.
   auto compute = [&](const WRegs& wc, int stage) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+      const uint16_t* bsrc = xs + stage * XS + (h ? bofs1 : bofs0);
+      bf16x8 bx[TM];
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) bx[mt] = *reinterpret_cast<const bf16x8*>(bsrc + mt * 1024);
+      __builtin_amdgcn_sched_barrier(0);
       bf16x8 aw[NMAT][TN];
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
         for (int nt = 0; nt < TN; ++nt) aw[mat][nt] = i8x8_to_bf16x8(wc[mat][nt][2 * h], wc[mat][nt][2 * h + 1]);
-      const uint16_t* bsrc = xs + stage * XS + (h ? bofs1 : bofs0);
 #pragma unroll
-      for (int mt = 0; mt < TM; ++mt) {
-        const bf16x8 bx = *reinterpret_cast<const bf16x8*>(bsrc + mt * 1024);
+      for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-          for (int nt = 0; nt < TN; ++nt) acc[mat][nt][mt] = mfma16x16x32(aw[mat][nt], bx, acc[mat][nt][mt]);
-      }
+          for (int nt = 0; nt < TN; ++nt) acc[mat][nt][mt] = mfma16x16x32(aw[mat][nt], bx[mt], acc[mat][nt][mt]);
     }
   };
 
