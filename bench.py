@@ -108,6 +108,63 @@ def per_call_sweep(layers, x, xo, xi, m):
     return step, per_layer_b * len(layers), per_layer_f * len(layers), 7 * len(layers)
 
 
+def torch_gpu_entry(ref_ms, dense_ms, ours_ms, work, unit):
+    """Report line for the torch comparison: the same work per sweep (this
+    package's algorithmic bytes or flops) over each path's time."""
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {
+        "what": "same 36-layer sweep with torch on this GPU: the reference's per-call dequantize "
+                "(engine/quantization.py:26-27) + F.linear, and F.linear on dense bf16 weights",
+        "reference_path_ms_per_step": round(ref_ms, 5),
+        "reference_path_rate": round(work / (ref_ms * 1e-3) / scale, 2),
+        "dense_bf16_ms_per_step": round(dense_ms, 5),
+        "dense_bf16_rate": round(work / (dense_ms * 1e-3) / scale, 2),
+        "unit": unit,
+        "speedup_vs_reference_path": round(ref_ms / ours_ms, 3),
+        "speedup_vs_dense_bf16": round(dense_ms / ours_ms, 3),
+    }
+
+
+def torch_reference_sweeps(layers, x, xo, steps):
+    """The reference's own computation with torch on this GPU, no kernel of
+    this package inside the timed graphs: per layer the 7 linears of
+    engine/model.py:168-190, each weight dequantized per call exactly as
+    engine/quantization.py:26-27 ((q.float() * scale).to(bf16)) and then
+    F.linear (hipBLASLt); and the same linears on weights dequantized once
+    beforehand (dense bf16, twice the weight bytes).  Returns ms per sweep."""
+    import torch.nn.functional as F
+
+    names = ("q", "k", "v", "o", "gate", "up", "down")
+    q8 = [{n: (L[n].q, L[n].scale.reshape(-1, 1)) for n in names} for L in layers]
+
+    def deq(q, s):
+        return (q.float() * s).to(torch.bfloat16)
+
+    def run(get):
+        y = None
+        for L, W in zip(layers, get):
+            F.linear(x, W("q"), L["q_b"])
+            F.linear(x, W("k"), L["k_b"])
+            F.linear(x, W("v"), L["v_b"])
+            F.linear(xo, W("o"))
+            act = F.silu(F.linear(x, W("gate"))) * F.linear(x, W("up"))
+            y = F.linear(act, W("down"))
+        return y
+
+    per_call = [(lambda d: (lambda n: deq(*d[n])))(d) for d in q8]
+    g, _ = capture(lambda: run(per_call))
+    ms_ref = time_graph(g, steps, 3)
+    del g
+    dense = [{n: deq(*d[n]) for n in names} for d in q8]
+    del q8, per_call
+    pre = [(lambda d: (lambda n: d[n]))(d) for d in dense]
+    g, _ = capture(lambda: run(pre))
+    ms_dense = time_graph(g, steps, 3)
+    del g, dense, pre
+    torch.cuda.empty_cache()
+    return ms_ref, ms_dense
+
+
 def reference_rms_norm(x, weight, eps):
     """engine/model.py:29-34 as the reference runs it (a chain of torch ops)."""
     dtype = x.dtype
@@ -212,12 +269,14 @@ def kernel_roofline(layers, launch, bytes_per_launch, flops_per_launch, bound, r
 # ---------------------------------------------------------------------------
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
-# summary key -> pattern on the demangled kernel name (the number-of-matrices
-# template argument is 2 for the gate|up pair)
+# summary key -> pattern on the demangled kernel name: the number-of-matrices
+# template argument is 2 for the gate|up pair (skinny_kernel<NW, U, NB, NMAT,
+# ...>, gemm_k64_kernel<BM, BN, NMAT, ...>; the profiler's demangler may drop
+# the first template argument, hence the optional group)
 PMC_KERNELS = {
     "copy": r"neg_kernel",
-    "skinny_gate_up_m1": r"skinny_kernel<\d+, \d+, 2,",
-    "gemm_gate_up_m512": r"gemm_k64_kernel<\d+, 2,|gemm_kernel<\d+, \d+, 2,",
+    "skinny_gate_up_m1": r"skinny_kernel<(\d+, )?\d+, \d+, 2, false",
+    "gemm_gate_up_m512": r"gemm_k64_kernel<(\d+, )?\d+, 2, false|gemm_kernel<(\d+, )?\d+, 2, false",
 }
 
 
@@ -411,6 +470,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "configs"], default="all")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workload sizes")
+    ap.add_argument("--no-torch-ref", action="store_true",
+                    help="skip the torch comparison sweeps (reference dequantize + F.linear, dense bf16)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the dispatches the rocprofv3 --pmc traffic passes read")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -476,6 +537,11 @@ def main():
             pval = pbytes / (pms * 1e-3) / 1e9
             log(f"[bench] per-call sweep (7 launches/layer): {pms * 1e3:.1f} us, {pval:.1f} GB/s")
             del g, pg
+            ref_ms = dense_ms = None
+            if not args.no_torch_ref:
+                ref_ms, dense_ms = torch_reference_sweeps(layers, x, xo, max(10, args.steps // 10))
+                log(f"[bench] reference computation with torch on this GPU: dequantize + F.linear "
+                    f"{ref_ms * 1e3:.1f} us, dense bf16 F.linear {dense_ms * 1e3:.1f} us per sweep")
             swiglu_b = 2 * INTER * HIDDEN + 8 * INTER + 2 * m * HIDDEN + 2 * m * INTER
             roof = kernel_roofline(layers, lambda L: Q.swiglu(x, L["gate"], L["up"]), swiglu_b,
                                    4 * m * INTER * HIDDEN, "hbm")
@@ -511,6 +577,8 @@ def main():
                                    "frac_of_hbm_peak": round(pval / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": pbytes, "launches_per_step": plaunch},
             })
+            if ref_ms is not None:
+                result["torch_gpu"] = torch_gpu_entry(ref_ms, dense_ms, ms, nbytes, "GB/s")
 
         # ---------------- prefill, M = prefill_m ----------------
         if args.only in ("all", "prefill") and args.prefill_m > 0:
@@ -525,6 +593,11 @@ def main():
             log(f"[bench] prefill m={pm}: {ms:.3f} ms/sweep, {tflops:.1f} TFLOP/s "
                 f"({100 * tflops / MFMA_BF16_PEAK_TFLOPS:.1f}% of bf16 MFMA peak)")
             del g
+            pref_ms = pdense_ms = None
+            if not args.no_torch_ref:
+                pref_ms, pdense_ms = torch_reference_sweeps(layers, px, pxo, 10)
+                log(f"[bench] prefill, reference computation with torch on this GPU: dequantize + F.linear "
+                    f"{pref_ms:.3f} ms, dense bf16 F.linear {pdense_ms:.3f} ms per sweep")
             proof = kernel_roofline(layers, lambda L: Q.swiglu(px, L["gate"], L["up"]),
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
@@ -534,6 +607,8 @@ def main():
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                                  "ms_per_step": round(ms, 5), "flops_per_step": nflops, "steps": psteps,
                                  "roofline": proof}
+            if pref_ms is not None:
+                result["prefill"]["torch_gpu"] = torch_gpu_entry(pref_ms, pdense_ms, ms, nflops, "TFLOP/s")
 
         # ---------------- the other workload sizes ----------------
         if args.only in ("all", "configs") and not args.no_configs:
@@ -568,7 +643,7 @@ def main():
                    "weight_dtype": "int8", "activation_dtype": "bf16", "accumulate": "fp32",
                    "parallelism": "none (1 GPU)"},
     }
-    for key in ("roofline", "cpu_baseline", "prefill", "per_call_sweep", "decode_detail", "other_configs"):
+    for key in ("roofline", "cpu_baseline", "prefill", "per_call_sweep", "torch_gpu", "decode_detail", "other_configs"):
         if key in result:
             line[key] = result[key]
     print(json.dumps(line), flush=True)
