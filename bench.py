@@ -174,26 +174,39 @@ def reference_rms_norm(x, weight, eps):
     return weight * xf.to(dtype)
 
 
-def layer_chain(layers, x0, attn, norms, fused):
+def reference_apply_rope(x, cos, sin):
+    """engine/model.py:37-39,53-56 (rotate_half, apply_rope), the torch op chain."""
+    x1, x2 = x.chunk(2, dim=-1)
+    return x * cos.unsqueeze(1) + torch.cat((-x2, x1), dim=-1) * sin.unsqueeze(1)
+
+
+def layer_chain(layers, x0, attn, norms, rope, fused):
     """The decoder layers' linears with their neighbours (engine/model.py:165-190,
-    attention replaced by a fixed input): norm -> q|k|v, x += o(attn),
-    norm -> gate|up -> down, x += down.  fused: the RMSNorm kernel and the
-    residual adds in the linear epilogues; otherwise the reference's torch op
-    chain and separate adds around the same linears."""
+    attention replaced by a fixed input): norm -> q|k|v -> RoPE of q and k,
+    x += o(attn), norm -> gate|up -> down, x += down.  fused: the RMSNorm and
+    RoPE kernels and the residual adds in the linear epilogues; otherwise the
+    reference's torch op chains and separate adds around the same linears."""
     from pageserve_amd import quantization as Q
+
+    cos, sin = rope
+    m = x0.shape[0]
+    heads, kv_heads, hd = HIDDEN // 128, KV // 128, 128
 
     def step():
         x = x0
         for L, (ln1, ln2) in zip(layers, norms):
             if fused:
                 h = Q.rmsnorm(x, ln1, 1e-6)
-                Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                q, k, _ = Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                Q.rope_qk(q.view(m, heads, hd), k.view(m, kv_heads, hd), cos, sin, inplace=True)
                 x = L["o"].linear(attn, residual=x)
                 h = Q.rmsnorm(x, ln2, 1e-6)
                 x = Q.mlp(h, L["gate"], L["up"], L["down"], residual=x)
             else:
                 h = reference_rms_norm(x, ln1, 1e-6)
-                Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                q, k, _ = Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+                reference_apply_rope(q.view(m, heads, hd), cos, sin)
+                reference_apply_rope(k.view(m, kv_heads, hd), cos, sin)
                 x = x + L["o"].linear(attn)
                 h = reference_rms_norm(x, ln2, 1e-6)
                 x = x + Q.mlp(h, L["gate"], L["up"], L["down"])
@@ -554,9 +567,13 @@ def main():
             ng = torch.Generator(device=dev).manual_seed(77)
             norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
                            for _ in range(2)) for _ in layers]
+            # rotary tables of the reference's cache (engine/model.py:42-47), one position
+            inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, device=dev).float() / 128))
+            emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
+            rope = (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
             chain = {}
             for fused in (False, True):
-                cg, _ = capture(layer_chain(layers, x, xo, norms, fused))
+                cg, _ = capture(layer_chain(layers, x, xo, norms, rope, fused))
                 chain[fused] = time_graph(cg, max(20, args.steps // 4), 5)
                 del cg
             log(f"[bench] decode layer chain with neighbours: fused {chain[True] * 1e3 / len(layers):.2f} us/layer, "
@@ -569,8 +586,8 @@ def main():
                                   "eager_gbs": round(nbytes / (ms_eager * 1e-3) / 1e9, 2),
                                   "down_proj_roofline": down_roof,
                                   "layer_chain_with_neighbours": {
-                                      "what": "per layer: rmsnorm, q|k|v, o + residual, rmsnorm, gate|up, down + "
-                                              "residual (attention output fixed); HIP-graph replay",
+                                      "what": "per layer: rmsnorm, q|k|v, RoPE of q and k, o + residual, rmsnorm, "
+                                              "gate|up, down + residual (attention output fixed); HIP-graph replay",
                                       "fused_us_per_layer": round(chain[True] * 1e3 / len(layers), 3),
                                       "reference_structure_us_per_layer": round(chain[False] * 1e3 / len(layers), 3)}},
                 "per_call_sweep": {"ms_per_step": round(pms, 5), "gbs": round(pval, 2),

@@ -164,6 +164,23 @@ int pgs_rmsnorm(const void* x, const void* weight, float eps, void* h,
                 int64_t m, int64_t k, void* stream);
 
 /*
+ * Replaces q = apply_rope(q, cos, sin); k = apply_rope(k, cos, sin) --
+ * engine/model.py:53-56 (apply_rope, rotate_half at :37-39), applied at
+ * :172-173 -- with one kernel for both tensors.  With h = head_dim / 2, per
+ * (token, head) and i < h, the reference's bf16 op chain
+ * x * cos + rotate_half(x) * sin with its roundings:
+ *   out[i]     = bf16( bf16(x[i]     * cos[i])     + bf16(-x[i + h] * sin[i]) )
+ *   out[i + h] = bf16( bf16(x[i + h] * cos[i + h]) + bf16( x[i]     * sin[i + h]) )
+ * q, q_out: bf16 [m, q_heads, head_dim]; k, k_out: bf16 [m, k_heads, head_dim]
+ * (k_heads = 0: q only); cos, sin: bf16 [m, head_dim], the rows of the
+ * reference's cos_cache / sin_cache for the m tokens.  Outputs may alias
+ * their inputs (in place).  head_dim even.
+ */
+int pgs_rope(const void* q, void* q_out, int64_t q_heads, const void* k, void* k_out,
+             int64_t k_heads, const void* cos, const void* sin, int64_t m,
+             int64_t head_dim, void* stream);
+
+/*
  * One output of a grouped linear: several quantized weights that read the
  * same activations (the q/k/v triple of engine/model.py:168-170).
  */

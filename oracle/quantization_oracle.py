@@ -194,6 +194,22 @@ def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     return round_to_bf16((np.asarray(weight, dtype=np.float32) * t).astype(np.float32))
 
 
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """``apply_rope(x, cos, sin)`` (engine/model.py:53-56, ``rotate_half`` at
+    :37-39) for bf16 tensors: ``x * cos + rotate_half(x) * sin`` where every
+    bf16 op computes in fp32 and rounds once.  x: (tokens, heads, head_dim)
+    float32 holding bf16 values; cos / sin: (tokens, head_dim) the same.
+    Returns float32 holding the bf16 result."""
+    x = np.asarray(x, np.float32)
+    h = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., h:], x[..., :h]], axis=-1)   # rotate_half: exact negation
+    c = np.asarray(cos, np.float32)[:, None, :]
+    s = np.asarray(sin, np.float32)[:, None, :]
+    t1 = round_to_bf16(x * c)
+    t2 = round_to_bf16(rot * s)
+    return round_to_bf16(t1 + t2)
+
+
 def linear_residual(x, q, scale, residual, bias=None, bf16_out: bool = True) -> np.ndarray:
     """``residual + F.linear(h, W, b)`` (engine/model.py:184, 190): the linear
     output is rounded to the output dtype first, then added to the bf16

@@ -8,6 +8,7 @@ computed by hand-written HIP kernels behind a C ABI
 from .quantization import (  # noqa: F401
     QuantizedWeight,
     W8A16Weight,
+    apply_rope,
     dequantize,
     linear,
     linear_group,
@@ -15,6 +16,7 @@ from .quantization import (  # noqa: F401
     mlp,
     quantize_per_channel,
     rmsnorm,
+    rope_qk,
     save_quantized,
     swiglu,
 )

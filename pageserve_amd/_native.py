@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class NativeLibraryError(RuntimeError):
@@ -63,6 +63,7 @@ SIGNATURES = {
     "pgs_w8a16_linear_group": (_INT, [_VP, ctypes.POINTER(LinearOut), _INT, _INT, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_w8a16_linear_residual": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_rmsnorm": (_INT, [_VP, _VP, ctypes.c_float, _VP, _I64, _I64, _VP]),
+    "pgs_rope": (_INT, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _VP, _I64, _I64, _VP]),
     "pgs_w8a16_swiglu": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_w8a16_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
 }

@@ -366,6 +366,66 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return h.reshape(x.shape)
 
 
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, m: int, head_dim: int, device) -> tuple:
+    if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
+        raise TypeError("rope: cos and sin must be bf16")
+    if tuple(cos.shape) != (m, head_dim) or tuple(sin.shape) != (m, head_dim):
+        raise ValueError(f"rope: cos and sin must be [{m}, {head_dim}]")
+    if cos.device != device or sin.device != device:
+        raise ValueError("rope: cos and sin must be on the tensors' device")
+    return cos.contiguous(), sin.contiguous()
+
+
+def _rope_input(x: torch.Tensor, name: str) -> torch.Tensor:
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise RuntimeError(f"rope: {name} must be on a ROCm GPU")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"rope: {name} must be bf16")
+    if x.dim() != 3:
+        raise ValueError(f"rope: {name} must be (tokens, heads, head_dim)")
+    return x.contiguous()
+
+
+def rope_qk(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+            inplace: bool = False) -> tuple:
+    """``q = apply_rope(q, cos, sin); k = apply_rope(k, cos, sin)``
+    (engine/model.py:53-56, applied at :172-173) in one launch, with the
+    reference's bf16 roundings.  q: (tokens, heads, head_dim) bf16, k:
+    (tokens, kv_heads, head_dim) bf16 or None; cos / sin: (tokens, head_dim)
+    bf16 (the reference's cache rows).  Returns (q_out, k_out); in place when
+    ``inplace`` (the inputs must then be contiguous)."""
+    qc = _rope_input(q, "q")
+    m, qh, hd = qc.shape
+    if k is not None:
+        kc = _rope_input(k, "k")
+        if kc.shape[0] != m or kc.shape[2] != hd or kc.device != qc.device:
+            raise ValueError("rope: k must match q in tokens, head_dim and device")
+        kh = kc.shape[1]
+    else:
+        kc, kh = None, 0
+    if hd % 2:
+        raise ValueError("rope: head_dim must be even")
+    if inplace and (qc is not q or (k is not None and kc is not k)):
+        raise ValueError("rope: in place needs contiguous q and k")
+    c, s = _rope_tables(cos, sin, m, hd, qc.device)
+    qo = qc if inplace else torch.empty_like(qc)
+    ko = (kc if inplace else torch.empty_like(kc)) if kc is not None else None
+    lib = _native.load()
+    with _on_device(qc.device):
+        stream = torch.cuda.current_stream(qc.device).cuda_stream
+        rc = lib.pgs_rope(_ptr(qc), _ptr(qo), qh, _ptr(kc) if kc is not None else None,
+                          _ptr(ko) if ko is not None else None, kh, _ptr(c), _ptr(s), m, hd,
+                          ctypes.c_void_p(stream))
+    check(rc, "rope")
+    return qo, ko
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """``apply_rope(x, cos, sin)`` of engine/model.py:53-56 as one kernel
+    (same arguments, same bf16 result)."""
+    return rope_qk(x, None, cos, sin)[0]
+
+
 def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list | None = None,
                  out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
     """Several projections of the same input in one launch (q/k/v,
