@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -53,15 +54,45 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# the compiler's per-kernel resource report (registers, scratch, occupancy)
+USAGE_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+
+def kernel_usage(stderr: str) -> dict:
+    """Kernel name -> {field: value} from the resource-usage remarks."""
+    usage, name = {}, None
+    for line in stderr.splitlines():
+        if "remark:" not in line or USAGE_FLAG not in line:
+            continue
+        body = line.split("remark:", 1)[1].rsplit("[", 1)[0].strip()
+        key, _, val = body.partition(":")
+        if key == "Function Name":
+            name = val.strip()
+            usage[name] = {}
+        elif name is not None:
+            usage[name][key.strip()] = val.strip()
+    return usage
+
+
 def _compile(hipcc: str, src: Path) -> Path:
     OBJDIR.mkdir(parents=True, exist_ok=True)
     obj = OBJDIR / (src.stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, USAGE_FLAG, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    # Every kernel is tuned to live in registers: a spill to scratch memory
+    # (after a change, or with another compiler) is a build error, not a
+    # silent slowdown.
+    spills = [f"{k}: scratch {u.get('ScratchSize [bytes/lane]')} B/lane, VGPR spill {u.get('VGPRs Spill')}"
+              for k, u in kernel_usage(res.stderr).items()
+              if u.get("ScratchSize [bytes/lane]", "0") != "0" or u.get("VGPRs Spill", "0") != "0"]
+    if spills:
+        raise RuntimeError(f"{src.name}: kernels spill registers to scratch:\n  " + "\n  ".join(spills))
     noise = "is not a recognized feature for this target"
-    warn = "\n".join(l for l in res.stderr.splitlines() if noise not in l and l.strip())
+    lines = [l for l in res.stderr.splitlines()
+             if l.strip() and noise not in l and USAGE_FLAG not in l and not re.match(r"^\s*\d*\s*\|", l)]
+    warn = "\n".join(lines)
     if warn:
         print(f"[pageserve_amd.build] {src.name}:\n{warn}", file=sys.stderr)
     return obj
