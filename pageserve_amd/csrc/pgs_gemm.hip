@@ -38,12 +38,6 @@ constexpr int kBK = 64;
 constexpr int kBN = 128;  // weight rows per tile and matrix: 4 waves x 32
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ int xcd_remap(int b, int total) {
-  const int xcd = b & 7, slot = b >> 3;
-  const int per = total >> 3, rem = total & 7;
-  return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-}
-
 // Element offset (bf16 units) of 16-byte chunk `ch` of row `row` in a
 // [rows][64] stage.  The chunk is XOR-swizzled with bits 0..2 of the row and
 // bit 3 folded into bit 0, so that the 16 lanes a 128-bit LDS access serves

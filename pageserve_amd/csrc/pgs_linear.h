@@ -49,7 +49,8 @@ struct SkinnyPlan {
   int tiles;   // 16-row tiles over all members
   int splits;  // workgroups per tile (split K across workgroups)
   bool pair;   // two K halves combined through pair slots (no reduce launch)
-  int shape;   // launch shape: waves per workgroup and chunks per wave
+  int shape;   // launch shape: waves per workgroup and K slots per wave
+  bool fold;   // two workgroups of 8 rows per tile, two chunks per MFMA (m <= 8)
 };
 
 // Launch plan of the tile GEMM (m > 16).
@@ -115,6 +116,16 @@ __device__ __forceinline__ T* pick_early(T* const (&arr)[L], int g) {
 #pragma unroll
   for (int i = 1; i < L; ++i) r = (g == i) ? v[i] : r;
   return (T*)r;
+}
+
+// Workgroup b of a grid of `total` runs on XCD b % 8 (round robin over the
+// eight XCDs); the remap numbers the workgroups of each XCD consecutively, so
+// that units with neighbouring numbers share an L2.  A bijection of
+// [0, total) for any total.
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+  const int xcd = b & 7, slot = b >> 3;
+  const int per = total >> 3, rem = total & 7;
+  return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
 __device__ __forceinline__ int member_of(const GroupArgs& a, int unit) {

@@ -15,8 +15,15 @@
 // fixed order.  Short-N shapes (o_proj, down_proj: 128 tiles) would leave
 // half of the 256 CUs idle, so their K range may be split over two
 // workgroups that meet in a pair slot (below); the SwiGLU pair splits
-// through workspace partials and a second small kernel instead.  Results
-// never depend on timing: every sum has a fixed order.
+// through workspace partials and a second small kernel instead.  At up to 8
+// tokens a short-N matrix is "folded" instead: two workgroups per tile, each
+// owning 8 of its rows over the whole K range, with two 64-k chunks per MFMA
+// (A rows 0-7: its rows in chunk c, A rows 8-15: the same rows in chunk c+1;
+// B columns 0..m-1: the tokens in chunk c, m..2m-1: the tokens in chunk c+1),
+// so that output (token t, row r) is C[r][t] + C[r+8][t+m].  Each lane's
+// 16 bytes are still one contiguous piece of the packed block, the
+// instruction stream equals that of a K split, and nothing crosses
+// workgroups.  Results never depend on timing: every sum has a fixed order.
 #include "pgs_linear.h"
 
 namespace pgs {
@@ -83,14 +90,20 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 // <= 80 registers.
 constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
 
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64>
+// FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
+// rows 8h .. 8h+7 of tile t.
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD>
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs) {
+  static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
-  const int tile = blockIdx.x / splits;
-  const int s = blockIdx.x - tile * splits;
+  // (folded: the two halves of a tile run back to back on one XCD)
+  const int unit = FOLD ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x / splits;
+  const int tile = FOLD ? unit >> 1 : unit;
+  const int half = FOLD ? unit & 1 : 0;
+  const int s = FOLD ? 0 : blockIdx.x - unit * splits;  // K split
 
   const int g = (NMAT == 2) ? 0 : member_of(a, tile);
   const int N = pick_early(a.n, g);
@@ -98,20 +111,26 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   const int lrow = lane & 15;
   const int kgrp = lane >> 4;
 
-  // one output per thread (M * 16 <= 256 <= 64 * NW)
+  // one output per thread (M * 16 <= 256 <= 64 * NW): token mm, tile row oi
   static_assert(NW >= 4, "the epilogue gives each thread at most one output");
   const int idx = threadIdx.x;
-  const int mm = idx >> 4, oi = idx & 15;
-  const bool has_out = idx < M * 16 && row0 + oi < N;
+  const int mm = FOLD ? idx >> 3 : idx >> 4;
+  const int oi = FOLD ? 8 * half + (idx & 7) : idx & 15;
+  const int nout = M * (FOLD ? 8 : 16);
+  const bool has_out = idx < nout && row0 + oi < N;
 
   // (splits <= 2 and nchunks <= 2^16: 32-bit arithmetic)
   const int nchunks = (K + 63) >> 6;
   const int cb = s * nchunks / splits;
   const int ce = (s + 1) * nchunks / splits;
-  // Packed weights: block (tile, chunk) is 1 KiB, this lane's 16 bytes at
-  // lane * 16.  One buffer resource per matrix spans exactly this
-  // workgroup's chunks [cb, ce) of its 16-row block row, so a chunk past the
-  // range reads zeros without touching memory.
+  // The range is walked in slots of S chunks (S = 2 folded: chunks
+  // cb + S*j .. cb + S*j + S-1 for slot j).
+  constexpr int S = FOLD ? 2 : 1;
+  const int nslots = (ce - cb + S - 1) / S;
+  // Packed weights: block (tile, chunk) is 1 KiB, the 16 bytes of tile row
+  // i, k group g at (i + 16 g) * 16.  One buffer resource per matrix spans
+  // exactly this workgroup's chunks [cb, ce) of its 16-row block row, so a
+  // chunk past the range reads zeros without touching memory.
   __amdgpu_buffer_rsrc_t wres[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
@@ -119,10 +138,16 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     wres[mat] = make_rsrc(qg + (static_cast<int64_t>(row0 >> 4) * nchunks + cb) * 1024,
                           static_cast<int64_t>(ce - cb) * 1024);
   }
-  const int woff = lane * 16;
-  // activations: row min(lrow, M - 1), this lane's 16 columns of each chunk
+  // A operand row lrow: tile row lrow, or (folded) row 8 half + lrow % 8 of
+  // the slot's chunk lrow / 8
+  const int woff = FOLD ? (lrow >> 3) * 1024 + (8 * half + (lrow & 7) + 16 * kgrp) * 16 : lane * 16;
+  // B operand column lrow: token min(lrow, M - 1), or (folded) token lrow % M
+  // of the slot's chunk lrow / M (columns >= 2M repeat column 0, unused); this
+  // lane's 16 k of the chunk
+  const int xsub = (FOLD && lrow >= M && lrow < 2 * M) ? 1 : 0;
+  const int xrow = FOLD ? (lrow < M ? lrow : (xsub ? lrow - M : 0)) : min(lrow, M - 1);
   const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<int64_t>(M) * K * 2);
-  const int xoff = min(lrow, M - 1) * K * 2 + kgrp * 32;
+  const int xoff = xrow * K * 2 + xsub * 128 + kgrp * 32;
 
   f32x4 acc[NMAT];
 #pragma unroll
@@ -138,8 +163,8 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     }
   };
 
-  // Batches of U chunks: batch j of this wave covers chunks c(j) .. c(j)+U-1,
-  // c(j) = cb + (j * NW + wave) * U.  Every load is issued and every MFMA
+  // Batches of U slots: batch j of this wave covers slots c(j) .. c(j)+U-1,
+  // c(j) = (j * NW + wave) * U.  Every load is issued and every MFMA
   // run unconditionally, in a fixed order (a chunk at or past ce reads zero
   // weights, and its activations are masked to zero as well, so that
   // non-finite inputs of other K ranges cannot leak in); with no branch the
@@ -156,26 +181,27 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   auto load_batch = [&](Batch& b, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int cc = c + u;
+      const int c0 = (c + u) * S;  // first chunk of the slot, from cb
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
-        b.w[u][mat] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff, (cc - cb) * 1024, kLoadNT);
-      // (K % 64 != 0: columns past K read the next row or zeros; mac_batch
-      // masks them)
-      b.x[u][0] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, cc * 128, 0);
-      b.x[u][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, cc * 128, 0);
+        b.w[u][mat] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff, c0 * 1024, kLoadNT);
+      // (chunks past the range, and K % 64 != 0 columns past K, read the
+      // next row or zeros; mac_batch masks them)
+      b.x[u][0] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, (cb + c0) * 128, 0);
+      b.x[u][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, (cb + c0) * 128, 0);
     }
   };
   auto mac_batch = [&](const Batch& b, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool on = c + u < ce && (K64 || (c + u) * 64 + kgrp * 16 < K);
+      const int ch = cb + (c + u) * S + xsub;  // this lane's activation chunk
+      const bool on = ch < ce && (K64 || ch * 64 + kgrp * 16 < K);
       const uint32_t mask = on ? 0xffffffffu : 0u;
       mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
     }
   };
   constexpr int kStep = NW * U;
-  const int first = cb + wave * U;
+  const int first = wave * U;
   // epilogue operands (clamped to a valid output, so the loads need no branch)
   auto load_epi = [&] { return epilogue_load<NMAT>(a, g, min(row0 + oi, N - 1), min(mm, M - 1), N, x); };
   EpiIn<NMAT> epi;
@@ -189,7 +215,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     for (int j = 0; j < NB; ++j) mac_batch(bt[j], first + j * kStep);
   } else {
     epi = load_epi();
-    for (int c = first; c < ce; c += 2 * kStep) {
+    for (int c = first; c < nslots; c += 2 * kStep) {
       Batch b0, b1;
       load_batch(b0, c);
       load_batch(b1, c + kStep);
@@ -203,14 +229,22 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   for (int mat = 0; mat < NMAT; ++mat) red[wave][mat][lane] = acc[mat];
   __syncthreads();
 
-  if (idx >= M * 16) return;
-  const int ln = acc_lane(oi, mm), r = oi & 3;
+  if (idx >= nout) return;
+  const int ln = acc_lane(FOLD ? oi & 7 : oi, mm), r = oi & 3;
   float v[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) t += red[w][mat][ln][r];
+    if constexpr (FOLD) {
+      // the second chunk of every slot: C[r + 8][mm + M]
+      const int ln2 = acc_lane((oi & 7) + 8, mm + M);
+      float t2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t2 += red[w][mat][ln2][r];
+      t += t2;
+    }
     v[mat] = t;
   }
   if (NMAT == 1 && pairs) {
@@ -263,30 +297,43 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
                                        reinterpret_cast<const uint16_t*>(pick_early(a.scale, g) + row0 + i)));
 }
 
-template <int NW, int U, int NB, int NMAT, bool OUT_F32>
-int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
-  const int64_t grid = static_cast<int64_t>(plan.tiles) * plan.splits;
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool FOLD>
+int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
+  const int64_t grid = static_cast<int64_t>(plan.tiles) * (FOLD ? 2 : plan.splits);
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
-  // NB > 0: the waves' batches must cover a workgroup's whole K range
-  const int per_wg = ((p.k + 63) / 64 + plan.splits - 1) / plan.splits;
-  if (NB > 0 && NB * U * NW < per_wg)
-    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: plan covers %d of %d chunks", NB * U * NW, per_wg);
   if (p.k % 64 == 0)
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
   else
-    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
-  int rc = check_launch("w8a16 skinny kernel");
+  return check_launch("w8a16 skinny kernel");
+}
+
+template <int NW, int U, int NB, int NMAT, bool OUT_F32>
+int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
+  if (plan.fold && (NMAT != 1 || plan.splits != 1 || plan.pair || p.m > 8))
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: folded plan for m=%d, %d matrices", p.m, NMAT);
+  // NB > 0: the waves' batches must cover a workgroup's whole K range
+  const int chunks = (p.k + 63) / 64;
+  const int per_wg = plan.fold ? (chunks + 1) / 2 : (chunks + plan.splits - 1) / plan.splits;
+  if (NB > 0 && NB * U * NW < per_wg)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: plan covers %d of %d slots", NB * U * NW, per_wg);
+  int rc;
+  if constexpr (NMAT == 1)
+    rc = plan.fold ? launch_kernel<NW, U, NB, NMAT, OUT_F32, true>(p, plan, st)
+                   : launch_kernel<NW, U, NB, NMAT, OUT_F32, false>(p, plan, st);
+  else
+    rc = launch_kernel<NW, U, NB, NMAT, OUT_F32, false>(p, plan, st);
   if (rc || plan.splits == 1 || plan.pair) return rc;
   hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT_F32>), dim3(static_cast<unsigned>(plan.tiles)), dim3(256), 0, st,
                      p.args, p.m, plan.splits, p.partials);
   return check_launch("w8a16 skinny reduce kernel");
 }
 
-// Launch shapes (waves per workgroup, chunks per batch, batches per wave);
-// a workgroup covers NW * U * NB chunks of 64 k.  Index kLoopShape: the
-// looping kernel for longer ranges.
+// Launch shapes (waves per workgroup, slots per batch, batches per wave);
+// a workgroup covers NW * U * NB slots of 64 k (128 k folded).  Index
+// kLoopShape: the looping kernel for longer ranges.
 struct SkinnyShape {
   int nw, u, nb;
 };
@@ -313,15 +360,24 @@ int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // Measured on MI355X inside HIP graphs (decode shapes of a 2048-hidden
   // model).  Every load of a workgroup is issued at once when its range fits
-  // one of the fixed shapes; fewer than 256 row tiles leave CUs idle, so a
-  // single matrix then splits K over two workgroups when K is long (down_proj:
-  // 7.1 vs 8.9 us) or when at most 128 tiles meet several tokens (o_proj at
-  // 16 tokens: 4.3 vs 4.8 us).  Otherwise a 32-chunk K is faster unsplit,
-  // without the pair slot's round trip (q|k|v, 160 tiles: 3.7 vs 4.2 us at
-  // one token, 4.9 vs 5.4 us at 16).
-  SkinnyPlan p{tiles, 1, false, kLoopShape};
+  // one of the fixed shapes; fewer than 256 row tiles leave CUs idle.  A
+  // single matrix then folds (8-row halves over the whole K, no combine) at
+  // up to 8 tokens, with two limits: the folded workgroup reads every token's
+  // activations over the whole K, so a long K folds at up to 4 tokens
+  // (down_proj: 6.6 vs 7.1 us paired at one token, 7.3 vs 7.4 at 4, 9.1 vs
+  // 8.1 at 8) and 129..255 tiles, which fill the CUs unsplit, only at up to 2
+  // (q|k|v at one token: 3.7 vs 3.8 us, at 4: 4.0 vs 3.9); o_proj: 3.2 vs
+  // 3.6 us at one token, 3.6 vs 4.0 at 8.  Past the fold, a single matrix
+  // splits K over two workgroups when K is long or when at most 128 tiles
+  // meet several tokens (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a
+  // 32-chunk K is faster unsplit, without the pair slot's round trip (q|k|v
+  // at 16 tokens: 4.9 vs 5.4 us).
+  SkinnyPlan p{tiles, 1, false, kLoopShape, false};
   const int chunks = (k + 63) / 64;
-  if (can_split && tiles < 256) {
+  if (nmat == 1 && chunks >= 16 && tiles < 256 && m <= 8 &&
+      (m <= 2 || (tiles <= 128 && (m <= 4 || chunks < 64)))) {
+    p.fold = true;
+  } else if (can_split && tiles < 256) {
     if (nmat == 1 && chunks >= 16 && (chunks >= 64 || (m > 4 && tiles <= 128))) {
       p.splits = 2;  // K halves combined through pair slots
       p.pair = true;
@@ -329,7 +385,7 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
       p.splits = 2;  // SwiGLU pair: partial tiles and a reduce kernel
     }
   }
-  const int per_wg = (chunks + p.splits - 1) / p.splits;
+  const int per_wg = p.fold ? (chunks + 1) / 2 : (chunks + p.splits - 1) / p.splits;
   // (the SwiGLU pair stops at 96 chunks: 128 would not fit its registers)
   const int last = nmat == 2 ? 4 : 5;
   for (int i = last; i >= 0; --i) {

@@ -42,6 +42,11 @@ SHAPES = [
     (20, 48, 16), (33, 130, 32), (40, 96, 48), (40, 256, 4112), (70, 2048, 11024),
     # 17..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also split)
     (70, 2048, 11008), (128, 2048, 11008), (96, 2560, 2048), (17, 300, 128),
+    # folded decode (8-row halves of a tile, two K chunks per MFMA, m <= 8):
+    # 2m = 16 columns, an odd chunk count with a K tail, 6 tokens
+    (3, 2048, 11008), (8, 130, 1040), (6, 48, 1104), (2, 2560, 2048),
+    # past the fold (paired K split): 8 tokens with a long K
+    (8, 2048, 11008),
 ]
 
 
@@ -121,18 +126,37 @@ def test_full_size_prefill_sampled(gpu):
 
 
 def test_paired_split_leaves_the_workspace_clean(gpu):
-    """Decode shapes with few row tiles split K in two and combine the halves
-    through slots at the front of the shared workspace; each call must leave
-    them empty.  Interleave differently shaped paired calls (o, down, a
-    ragged one, 16 tokens) and repeat: every result must match the oracle."""
+    """Decode shapes with few row tiles at 9..16 tokens split K in two and
+    combine the halves through slots at the front of the shared workspace;
+    each call must leave them empty.  Interleave differently shaped paired
+    calls (o, down, a ragged one) with folded ones (up to 8 tokens, no
+    slots) and repeat: every result must match the oracle."""
     cases = [_problem(gpu, 300 + j, m, n, k) for j, (m, n, k) in
-             enumerate([(1, 2048, 2048), (1, 2048, 11008), (3, 1000, 1040), (16, 256, 2048), (1, 33, 1024)])]
+             enumerate([(1, 2048, 2048), (12, 2048, 11008), (9, 1000, 1040), (16, 256, 2048), (1, 33, 1024),
+                        (16, 2048, 2048), (3, 1000, 1040)])]
     xs = [bf16_gpu(c[3], gpu) for c in cases]
     refs = [O.linear(c[3], c[1], c[2]) for c in cases]
     for rep in range(3):
         outs = [c[0].linear(x) for c, x in zip(cases, xs)]
         for (qw, q, s, x, _), y, ref in zip(cases, outs, refs):
             report(to_np(y), ref, x.shape[1], f"paired m={x.shape[0]} n={q.shape[0]} k={x.shape[1]} rep={rep}")
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48)])
+def test_nonfinite_token_stays_in_its_row(gpu, m, n, k):
+    """A token whose activations hold inf and nan poisons only its own
+    outputs (as in x @ W^T): padding columns and the K range of another
+    workgroup or MFMA column must not carry it into the other tokens."""
+    qw, q, s, x, _ = _problem(gpu, 90, m, n, k)
+    bad = m // 2
+    x = x.copy()
+    x[bad, :16] = np.inf
+    x[bad, -16:] = np.nan
+    y = to_np(qw.linear(bf16_gpu(x, gpu)))
+    ok = [t for t in range(m) if t != bad]
+    assert not np.isfinite(y[bad]).any()
+    ref = O.linear(x[ok], q, s)
+    report(y[ok], ref, k, f"non-finite token m={m} n={n} k={k}")
 
 
 def test_deterministic(gpu):

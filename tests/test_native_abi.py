@@ -81,16 +81,19 @@ def test_missing_library_fails_loudly(tmp_path):
 
 
 def test_workspace_query(native_lib):
-    """Short-N decode shapes split K and need a workspace; wide ones do not."""
+    """Short-N shapes at 9..16 tokens split K and need a workspace; at up
+    to 8 tokens they fold (no workspace), and wide ones do not split."""
     def need(m, ns, k, swiglu=0):
         arr = (ctypes.c_int64 * len(ns))(*ns)
         return native_lib.pgs_w8a16_workspace_bytes(m, arr, len(ns), k, swiglu)
 
-    assert need(1, [2048], 11008) > 0                           # down_proj at decode
+    assert need(16, [2048], 11008) > 0                          # down_proj at 16 tokens: K split
+    assert need(1, [2048], 11008) == 0                          # down_proj at 1 token: folded
     assert need(1, [151936], 2048) == 0                         # lm_head: plenty of tiles
     assert need(0, [2048], 2048) == 0 and need(1, [2048], -5) == 0
     assert need(1, [0], 2048) == 0
-    assert need(4, [2048, 256, 256], 2048) >= need(4, [2048], 2048)
+    assert need(12, [1024, 256, 256], 2048) >= need(12, [2048], 2048) > 0   # o / a small q|k|v group
+    assert need(8, [1024, 256, 256], 2048) == 0                 # folded
 
 
 @pytest.mark.parametrize("n,k,expect", [(16, 64, 1024), (17, 64, 2048), (16, 65, 2048), (0, 64, 0), (2048, 11008,
