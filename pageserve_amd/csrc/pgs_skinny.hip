@@ -358,20 +358,21 @@ int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
 }  // namespace
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
-  // Measured on MI355X inside HIP graphs (decode shapes of a 2048-hidden
-  // model).  Every load of a workgroup is issued at once when its range fits
-  // one of the fixed shapes; fewer than 256 row tiles leave CUs idle.  A
-  // single matrix then folds (8-row halves over the whole K, no combine) at
-  // up to 8 tokens, with two limits: the folded workgroup reads every token's
-  // activations over the whole K, so a long K folds at up to 4 tokens
-  // (down_proj: 6.6 vs 7.1 us paired at one token, 7.3 vs 7.4 at 4, 9.1 vs
-  // 8.1 at 8) and 129..255 tiles, which fill the CUs unsplit, only at up to 2
-  // (q|k|v at one token: 3.7 vs 3.8 us, at 4: 4.0 vs 3.9); o_proj: 3.2 vs
-  // 3.6 us at one token, 3.6 vs 4.0 at 8.  Past the fold, a single matrix
-  // splits K over two workgroups when K is long or when at most 128 tiles
-  // meet several tokens (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a
-  // 32-chunk K is faster unsplit, without the pair slot's round trip (q|k|v
-  // at 16 tokens: 4.9 vs 5.4 us).
+  // Measured on MI355X inside HIP graphs that cycle > 512 MB of distinct
+  // weights (decode shapes of a 2048-hidden model).  Every load of a
+  // workgroup is issued at once when its range fits one of the fixed shapes;
+  // fewer than 256 row tiles leave CUs idle.  A single matrix then folds
+  // (8-row halves over the whole K, no combine) at up to 8 tokens, with two
+  // limits: the folded workgroup reads every token's activations over the
+  // whole K, so a long K folds at up to 4 tokens (down_proj: 6.6 vs 7.1 us
+  // paired at one token, 7.2 vs 7.4 at 4, 9.1 vs 8.1 at 8) and 129..255
+  // tiles, which fill the CUs unsplit, only at up to 2 (q|k|v at one token:
+  // 3.55 vs 3.62 us, at 4: 3.83 vs 3.82); o_proj: 3.0 vs 3.4 us at one token,
+  // 3.4 vs 4.0 at 8.  Past the fold, a single matrix splits K over two
+  // workgroups when K is long or when at most 128 tiles meet several tokens
+  // (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a 32-chunk K is faster
+  // unsplit, without the pair slot's round trip (q|k|v at 16 tokens: 4.7 vs
+  // 5.4 us).
   SkinnyPlan p{tiles, 1, false, kLoopShape, false};
   const int chunks = (k + 63) / 64;
   if (nmat == 1 && chunks >= 16 && tiles < 256 && m <= 8 &&
