@@ -91,12 +91,14 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
 
 // FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
-// rows 8h .. 8h+7 of tile t.
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD>
+// rows 8h .. 8h+7 of tile t.  ONE: a single token (M == 1, NB > 0, K % 64 ==
+// 0, folded), its activations staged through LDS (below).
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, bool ONE>
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
+  static_assert(!ONE || (NB > 0 && K64 && FOLD), "single-token staging covers folded issue-once shapes");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   // (folded: the two halves of a tile run back to back on one XCD)
@@ -178,6 +180,13 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     u32x4 w[U][NMAT];
     u32x4 x[U][2];
   };
+  auto load_w = [&](Batch& b, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+        b.w[u][mat] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff, (c + u) * S * 1024, kLoadNT);
+  };
   auto load_batch = [&](Batch& b, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -191,13 +200,31 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
       b.x[u][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, (cb + c0) * 128, 0);
     }
   };
-  auto mac_batch = [&](const Batch& b, int c) {
+
+  // ONE: the single token's activations for this wave's NB * U slots
+  // (S chunk rows of 128 bytes each) are fetched once, as XP 16-byte pieces
+  // (piece p by lane p % 64 in pass p / 64), parked in the wave's own slice
+  // of LDS and read back as B operands, all 16 lanes of a k group from one
+  // address (an LDS broadcast).  That replaces two vector loads per chunk,
+  // each returning 1 KiB to the registers of which the one real column uses
+  // 64 bytes, by XPASS loads per wave.  Only this wave touches its slice.
+  constexpr int XP = ONE ? NB * U * S * 8 : 1;
+  constexpr int XPASS = (XP + 63) / 64;
+  __shared__ u32x4 xst[ONE ? NW * XPASS * 64 : 1];
+  u32x4* const xw = xst + (ONE ? wave * XPASS * 64 : 0);
+
+  auto mac_batch = [&](const Batch& b, int c, int j) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int ch = cb + (c + u) * S + xsub;  // this lane's activation chunk
       const bool on = ch < ce && (K64 || ch * 64 + kgrp * 16 < K);
       const uint32_t mask = on ? 0xffffffffu : 0u;
-      mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
+      if constexpr (ONE) {
+        const u32x4* src = xw + ((j * U + u) * S + xsub) * 8 + kgrp * 2;
+        mac(b.w[u], src[0] & mask, src[1] & mask);
+      } else {
+        mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
+      }
     }
   };
   constexpr int kStep = NW * U;
@@ -207,20 +234,44 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   EpiIn<NMAT> epi;
   if constexpr (NB > 0) {
     Batch bt[NB];
+    u32x4 xpiece[ONE ? XPASS : 1];
+    if constexpr (ONE) {
+      // the pieces first, so that parking them waits for them alone
 #pragma unroll
-    for (int j = 0; j < NB; ++j) load_batch(bt[j], first + j * kStep);
+      for (int i = 0; i < XPASS; ++i) {
+        const int p = lane + 64 * i;
+        const int sw = p / (S * 8), r = p % (S * 8);  // slot of the wave, piece in the slot
+        const int ch = cb + (first + (sw / U) * kStep + sw % U) * S + (r >> 3);
+        // (pieces past XP, and chunks past K, read zeros)
+        const int off = p < XP ? ch * 128 + (r & 7) * 16 : 0x7ffffff0;
+        xpiece[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) load_w(bt[j], first + j * kStep);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) load_batch(bt[j], first + j * kStep);
+    }
     epi = load_epi();  // behind the weight loads
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+    if constexpr (ONE) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) mac_batch(bt[j], first + j * kStep);
+      for (int i = 0; i < XPASS; ++i) xw[lane + 64 * i] = xpiece[i];
+      // the same wave reads the slice back: its LDS operations complete in
+      // order; keep the compiler from moving the reads above the stores
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) mac_batch(bt[j], first + j * kStep, j);
   } else {
     epi = load_epi();
     for (int c = first; c < nslots; c += 2 * kStep) {
       Batch b0, b1;
       load_batch(b0, c);
       load_batch(b1, c + kStep);
-      mac_batch(b0, c);
-      mac_batch(b1, c + kStep);
+      mac_batch(b0, c, 0);
+      mac_batch(b1, c + kStep, 0);
     }
   }
 
@@ -301,12 +352,24 @@ template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool FOLD>
 int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * (FOLD ? 2 : plan.splits);
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
+  const dim3 g(static_cast<unsigned>(grid)), b(64 * NW);
+  // A single token in a folded launch stages its activations through LDS
+  // (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 -> 3.38,
+  // o_proj 2.97 -> 3.03; the unfolded SwiGLU pair, 4 chunks per wave, loses:
+  // 9.21 -> 9.33 us, so it keeps direct loads).
+  if constexpr (NB > 0 && FOLD) {
+    if (p.k % 64 == 0 && p.m == 1) {
+      hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, true>), g, b, 0, st, p.x, p.args, p.m,
+                         p.k, plan.splits, p.partials, pairs);
+      return check_launch("w8a16 skinny kernel");
+    }
+  }
   if (p.k % 64 == 0)
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
+    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, false>), g, b, 0, st, p.x, p.args, p.m,
+                       p.k, plan.splits, p.partials, pairs);
   else
-    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs);
+    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, false>), g, b, 0, st, p.x, p.args, p.m,
+                       p.k, plan.splits, p.partials, pairs);
   return check_launch("w8a16 skinny kernel");
 }
 
