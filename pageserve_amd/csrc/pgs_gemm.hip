@@ -70,6 +70,67 @@ __device__ __forceinline__ void store_partials(const f32x4 (&acc)[NMAT][TN][TM],
       for (int mt = 0; mt < TM; ++mt) part[mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
 }
 
+// Epilogue operands of four consecutive output rows nb .. nb+3 (clamped to
+// N - 1 past the end): scales, bias (single matrices) or the pair's second
+// scale.
+template <int NMAT>
+struct Rows4 {
+  float s0[4], s1[4], bv[4];
+};
+template <int NMAT>
+__device__ __forceinline__ Rows4<NMAT> rows4(const GroupArgs& a, int g, int N, int nb) {
+  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
+  const float* sc1 = a.scale[NMAT - 1];
+  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
+  Rows4<NMAT> e;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = min(nb + r, N - 1);
+    e.s0[r] = sc0[n];
+    e.s1[r] = (NMAT == 2) ? sc1[n] : 0.f;
+    e.bv[r] = (NMAT == 1 && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
+  }
+  return e;
+}
+
+// Rows nb .. nb+3 of token m from their fp32 sums: scale and bias, or SwiGLU,
+// then the residual (single matrices) and one vector store when the four
+// outputs are in range and aligned (`yvec`), else element stores.
+template <int NMAT, bool OUT_F32>
+__device__ __forceinline__ void store_rows4(const GroupArgs& a, int g, int N, int m, int nb, const Rows4<NMAT>& e,
+                                            const f32x4& v0, const f32x4& v1, void* y, bool yvec) {
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if constexpr (NMAT == 2)
+      v[r] = silu_f32(v0[r] * e.s0[r]) * (v1[r] * e.s1[r]);
+    else
+      v[r] = v0[r] * e.s0[r] + e.bv[r];
+  }
+  const int64_t base = static_cast<int64_t>(m) * N + nb;
+  const uint16_t* res = (NMAT == 2) ? nullptr : pick(a.res, g);
+  if (NMAT == 1 && res) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = add_residual<OUT_F32>(v[r], res, base + min(r, N - 1 - nb));
+  }
+  if (yvec && nb + 3 < N) {
+    if constexpr (OUT_F32)
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
+    else
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + base) =
+          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < N) store_out<OUT_F32>(y, base + r, v[r]);
+  }
+}
+
+template <bool OUT_F32>
+__device__ __forceinline__ bool vec_out(const void* y, int N) {
+  return (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
+}
+
 // Epilogue of one workgroup tile: lane (lr, lg) of wave `wave` holds, for
 // weight tile nt and token tile mt, rows nb + r (r = 0..3) of token
 // m0 + mt*16 + lr, nb = n0 + wave*BN/4 + nt*16 + 4*lg.  Applies scale, bias
@@ -77,51 +138,17 @@ __device__ __forceinline__ void store_partials(const f32x4 (&acc)[NMAT][TN][TM],
 template <int BN, int TN, int TM, int NMAT, bool OUT_F32>
 __device__ __forceinline__ void store_tile(const f32x4 (&acc)[NMAT][TN][TM], const GroupArgs& a, int g, int M,
                                            int N, int m0, int n0, int wave, int lr, int lg) {
-  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
-  const float* sc1 = a.scale[NMAT - 1];
-  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
-  const uint16_t* res = (NMAT == 2) ? nullptr : pick(a.res, g);
   void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
-  const bool yvec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & (OUT_F32 ? 15 : 7)) == 0;
+  const bool yvec = vec_out<OUT_F32>(y, N);
 #pragma unroll
   for (int nt = 0; nt < TN; ++nt) {
     const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * lg;
-    float s0[4], s1[4], bv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = min(nb + r, N - 1);
-      s0[r] = sc0[n];
-      s1[r] = (NMAT == 2) ? sc1[n] : 0.f;
-      bv[r] = (NMAT == 1 && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
-    }
+    const Rows4<NMAT> e = rows4<NMAT>(a, g, N, nb);
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt) {
       const int m = m0 + mt * 16 + lr;
       if (m >= M) continue;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (NMAT == 2)
-          v[r] = silu_f32(acc[0][nt][mt][r] * s0[r]) * (acc[NMAT - 1][nt][mt][r] * s1[r]);
-        else
-          v[r] = acc[0][nt][mt][r] * s0[r] + bv[r];
-      }
-      const int64_t base = static_cast<int64_t>(m) * N + nb;
-      if (NMAT == 1 && res) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = add_residual<OUT_F32>(v[r], res, base + min(r, N - 1 - nb));
-      }
-      if (yvec && nb + 3 < N) {
-        if constexpr (OUT_F32)
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + base) = f32x4{v[0], v[1], v[2], v[3]};
-        else
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + base) =
-              u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < N) store_out<OUT_F32>(y, base + r, v[r]);
-      }
+      store_rows4<NMAT, OUT_F32>(a, g, N, m, nb, e, acc[0][nt][mt], acc[NMAT - 1][nt][mt], y, yvec);
     }
   }
 }
@@ -598,24 +625,8 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
     v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int sp = 0; sp < ga.splits; ++sp) v[mat] += part[(static_cast<int64_t>(sp) * NMAT + mat) * SLOTS + slot];
   }
-  const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
-  const float* sc1 = a.scale[NMAT - 1];
-  const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
   void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int n = nb + r;
-    if (n >= N) continue;
-    float o;
-    if constexpr (NMAT == 2) {
-      o = silu_f32(v[0][r] * sc0[n]) * (v[NMAT - 1][r] * sc1[n]);
-    } else {
-      o = v[0][r] * sc0[n];
-      if (bias) o += bf16_bits_to_f32(bias[n]);
-      o = add_residual<OUT_F32>(o, pick(a.res, g), static_cast<int64_t>(m) * N + n);
-    }
-    store_out<OUT_F32>(y, static_cast<int64_t>(m) * N + n, o);
-  }
+  store_rows4<NMAT, OUT_F32>(a, g, N, m, nb, rows4<NMAT>(a, g, N, nb), v[0], v[NMAT - 1], y, vec_out<OUT_F32>(y, N));
 }
 
 template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
