@@ -10,6 +10,8 @@ residual epilogue.  Sizes are capped so the float64 oracle stays fast.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -20,7 +22,8 @@ from pageserve_amd import quantization as Q
 
 pytestmark = pytest.mark.gpu
 
-CASES = 40
+# PGS_RANDOM_CASES raises the count for a longer soak of the launch plans
+CASES = int(os.environ.get("PGS_RANDOM_CASES", "40"))
 MAX_WORK = 1.2e8  # m * n * k of the oracle's float64 product
 
 
