@@ -91,14 +91,14 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
 
 // FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
-// rows 8h .. 8h+7 of tile t.  ONE: a single token (M == 1, NB > 0, K % 64 ==
-// 0, folded), its activations staged through LDS (below).
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, bool ONE>
+// rows 8h .. 8h+7 of tile t.  XM > 0: up to XM tokens (M <= XM, NB > 0, K %
+// 64 == 0, folded), their activations staged through LDS (below).
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM>
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
-  static_assert(!ONE || (NB > 0 && K64 && FOLD), "single-token staging covers folded issue-once shapes");
+  static_assert(XM == 0 || (NB > 0 && K64 && FOLD), "activation staging covers folded issue-once shapes");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   // (folded: the two halves of a tile run back to back on one XCD)
@@ -201,17 +201,21 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     }
   };
 
-  // ONE: the single token's activations for this wave's NB * U slots
-  // (S chunk rows of 128 bytes each) are fetched once, as XP 16-byte pieces
+  // XM > 0: the tokens' activations for this wave's NB * U slots (S chunk
+  // rows of 128 bytes per token) are fetched once, as XP 16-byte pieces
   // (piece p by lane p % 64 in pass p / 64), parked in the wave's own slice
-  // of LDS and read back as B operands, all 16 lanes of a k group from one
-  // address (an LDS broadcast).  That replaces two vector loads per chunk,
-  // each returning 1 KiB to the registers of which the one real column uses
-  // 64 bytes, by XPASS loads per wave.  Only this wave touches its slice.
-  constexpr int XP = ONE ? NB * U * S * 8 : 1;
+  // of LDS and read back as B operands.  That replaces two vector loads per
+  // chunk, each returning 1 KiB to the registers although the M real columns
+  // use M * 64 bytes of it (M = 1: all 16 lanes of a k group read one
+  // address, an LDS broadcast), by XPASS loads per wave.  Only this wave
+  // touches its slice.  Slice layout: row (slot chunk, token) of 8 pieces,
+  // rows 9 pieces apart, so that the B reads of up to eight rows (XM tokens
+  // x 2 chunks) fall on distinct banks.
+  constexpr int XP = XM > 0 ? NB * U * S * XM * 8 : 1;
   constexpr int XPASS = (XP + 63) / 64;
-  __shared__ u32x4 xst[ONE ? NW * XPASS * 64 : 1];
-  u32x4* const xw = xst + (ONE ? wave * XPASS * 64 : 0);
+  constexpr int XROWS = XM > 0 ? NB * U * S * XM : 1;
+  __shared__ u32x4 xst[XM > 0 ? NW * XROWS * 9 : 1];
+  u32x4* const xw = xst + (XM > 0 ? wave * XROWS * 9 : 0);
 
   auto mac_batch = [&](const Batch& b, int c, int j) {
 #pragma unroll
@@ -219,8 +223,8 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
       const int ch = cb + (c + u) * S + xsub;  // this lane's activation chunk
       const bool on = ch < ce && (K64 || ch * 64 + kgrp * 16 < K);
       const uint32_t mask = on ? 0xffffffffu : 0u;
-      if constexpr (ONE) {
-        const u32x4* src = xw + ((j * U + u) * S + xsub) * 8 + kgrp * 2;
+      if constexpr (XM > 0) {
+        const u32x4* src = xw + (((j * U + u) * S + xsub) * XM + xrow) * 9 + kgrp * 2;
         mac(b.w[u], src[0] & mask, src[1] & mask);
       } else {
         mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
@@ -234,16 +238,19 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   EpiIn<NMAT> epi;
   if constexpr (NB > 0) {
     Batch bt[NB];
-    u32x4 xpiece[ONE ? XPASS : 1];
-    if constexpr (ONE) {
+    u32x4 xpiece[XM > 0 ? XPASS : 1];
+    if constexpr (XM > 0) {
       // the pieces first, so that parking them waits for them alone
 #pragma unroll
       for (int i = 0; i < XPASS; ++i) {
         const int p = lane + 64 * i;
-        const int sw = p / (S * 8), r = p % (S * 8);  // slot of the wave, piece in the slot
-        const int ch = cb + (first + (sw / U) * kStep + sw % U) * S + (r >> 3);
-        // (pieces past XP, and chunks past K, read zeros)
-        const int off = p < XP ? ch * 128 + (r & 7) * 16 : 0x7ffffff0;
+        // piece p: 16-byte piece p % 8 of token (p / 8) % XM in chunk row
+        // p / (8 XM) (slot of the wave, then chunk of the slot)
+        const int t = (p >> 3) % XM, cr = p / (8 * XM);
+        const int sw = cr / S;
+        const int ch = cb + (first + (sw / U) * kStep + sw % U) * S + cr % S;
+        // (pieces past XP, tokens past M and chunks past K read zeros)
+        const int off = p < XP ? t * K * 2 + ch * 128 + (p & 7) * 16 : 0x7ffffff0;
         xpiece[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0);
       }
 #pragma unroll
@@ -254,9 +261,12 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     }
     epi = load_epi();  // behind the weight loads
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
-    if constexpr (ONE) {
+    if constexpr (XM > 0) {
 #pragma unroll
-      for (int i = 0; i < XPASS; ++i) xw[lane + 64 * i] = xpiece[i];
+      for (int i = 0; i < XPASS; ++i) {
+        const int p = lane + 64 * i;
+        if (p < XP) xw[(p >> 3) * 9 + (p & 7)] = xpiece[i];
+      }
       // the same wave reads the slice back: its LDS operations complete in
       // order; keep the compiler from moving the reads above the stores
       __builtin_amdgcn_wave_barrier();
@@ -353,22 +363,29 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * (FOLD ? 2 : plan.splits);
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
   const dim3 g(static_cast<unsigned>(grid)), b(64 * NW);
-  // A single token in a folded launch stages its activations through LDS
-  // (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 -> 3.38,
-  // o_proj 2.97 -> 3.03; the unfolded SwiGLU pair, 4 chunks per wave, loses:
-  // 9.21 -> 9.33 us, so it keeps direct loads).
+  // Up to four tokens in a folded launch stage their activations through
+  // LDS (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 ->
+  // 3.38, o_proj 2.97 -> 3.03; the unfolded SwiGLU pair, 4 chunks per wave,
+  // loses: 9.21 -> 9.33 us, so it keeps direct loads).
   if constexpr (NB > 0 && FOLD) {
-    if (p.k % 64 == 0 && p.m == 1) {
-      hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, true>), g, b, 0, st, p.x, p.args, p.m,
-                         p.k, plan.splits, p.partials, pairs);
+    if (p.k % 64 == 0 && p.m <= 4) {
+      if (p.m == 1)
+        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1>), g, b, 0, st, p.x, p.args, p.m,
+                           p.k, plan.splits, p.partials, pairs);
+      else if (p.m == 2)
+        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2>), g, b, 0, st, p.x, p.args, p.m,
+                           p.k, plan.splits, p.partials, pairs);
+      else
+        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4>), g, b, 0, st, p.x, p.args, p.m,
+                           p.k, plan.splits, p.partials, pairs);
       return check_launch("w8a16 skinny kernel");
     }
   }
   if (p.k % 64 == 0)
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, false>), g, b, 0, st, p.x, p.args, p.m,
+    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0>), g, b, 0, st, p.x, p.args, p.m,
                        p.k, plan.splits, p.partials, pairs);
   else
-    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, false>), g, b, 0, st, p.x, p.args, p.m,
+    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, 0>), g, b, 0, st, p.x, p.args, p.m,
                        p.k, plan.splits, p.partials, pairs);
   return check_launch("w8a16 skinny kernel");
 }

@@ -47,8 +47,8 @@ SHAPES = [
     (3, 2048, 11008), (8, 130, 1040), (6, 48, 1104), (2, 2560, 2048),
     # past the fold (paired K split): 8 tokens with a long K
     (8, 2048, 11008),
-    # one token, folded, activations staged through LDS: odd chunk counts
-    (1, 2048, 1088), (1, 300, 4160),
+    # one to four tokens, folded, activations staged through LDS: odd chunk counts
+    (1, 2048, 1088), (1, 300, 4160), (2, 2048, 1088), (4, 300, 4160), (3, 130, 2112),
 ]
 
 
