@@ -180,12 +180,14 @@ def reference_apply_rope(x, cos, sin):
     return x * cos.unsqueeze(1) + torch.cat((-x2, x1), dim=-1) * sin.unsqueeze(1)
 
 
-def layer_chain(layers, x0, attn, norms, rope, fused):
+def layer_chain(layers, x0, attn, norms, rope, mode):
     """The decoder layers' linears with their neighbours (engine/model.py:165-190,
     attention replaced by a fixed input): norm -> q|k|v -> RoPE of q and k,
-    x += o(attn), norm -> gate|up -> down, x += down.  fused: the RMSNorm and
-    RoPE kernels and the residual adds in the linear epilogues; otherwise the
-    reference's torch op chains and separate adds around the same linears."""
+    x += o(attn), norm -> gate|up -> down, x += down.  mode "reference": the
+    reference's torch op chains and separate adds around the same linears;
+    "kernels": the RMSNorm and RoPE kernels and the residual adds in the
+    linear epilogues; "norm_in_linear": as "kernels" with each RMSNorm inside
+    the projection launch that consumes it."""
     from pageserve_amd import quantization as Q
 
     cos, sin = rope
@@ -195,7 +197,13 @@ def layer_chain(layers, x0, attn, norms, rope, fused):
     def step():
         x = x0
         for L, (ln1, ln2) in zip(layers, norms):
-            if fused:
+            if mode == "norm_in_linear":
+                q, k, _ = Q.rmsnorm_linear_group(x, ln1, 1e-6, [L["q"], L["k"], L["v"]],
+                                                 [L["q_b"], L["k_b"], L["v_b"]])
+                Q.rope_qk(q.view(m, heads, hd), k.view(m, kv_heads, hd), cos, sin, inplace=True)
+                x = L["o"].linear(attn, residual=x)
+                x = Q.rmsnorm_mlp(x, ln2, 1e-6, L["gate"], L["up"], L["down"], residual=x)
+            elif mode == "kernels":
                 h = Q.rmsnorm(x, ln1, 1e-6)
                 q, k, _ = Q.linear_group(h, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
                 Q.rope_qk(q.view(m, heads, hd), k.view(m, kv_heads, hd), cos, sin, inplace=True)
@@ -572,12 +580,12 @@ def main():
             emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
             rope = (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
             chain = {}
-            for fused in (False, True):
-                cg, _ = capture(layer_chain(layers, x, xo, norms, rope, fused))
-                chain[fused] = time_graph(cg, max(20, args.steps // 4), 5)
+            for mode in ("reference", "kernels", "norm_in_linear"):
+                cg, _ = capture(layer_chain(layers, x, xo, norms, rope, mode))
+                chain[mode] = time_graph(cg, max(20, args.steps // 4), 5) * 1e3 / len(layers)
                 del cg
-            log(f"[bench] decode layer chain with neighbours: fused {chain[True] * 1e3 / len(layers):.2f} us/layer, "
-                f"reference structure {chain[False] * 1e3 / len(layers):.2f} us/layer")
+            log(f"[bench] decode layer chain with neighbours (us/layer): norm in the linear {chain['norm_in_linear']:.2f}"
+                f", separate kernels {chain['kernels']:.2f}, reference structure {chain['reference']:.2f}")
             result.update({
                 "value": round(value, 2), "ms_per_step": round(ms, 5), "roofline": roof,
                 "decode_detail": {"frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
@@ -588,8 +596,9 @@ def main():
                                   "layer_chain_with_neighbours": {
                                       "what": "per layer: rmsnorm, q|k|v, RoPE of q and k, o + residual, rmsnorm, "
                                               "gate|up, down + residual (attention output fixed); HIP-graph replay",
-                                      "fused_us_per_layer": round(chain[True] * 1e3 / len(layers), 3),
-                                      "reference_structure_us_per_layer": round(chain[False] * 1e3 / len(layers), 3)}},
+                                      "fused_us_per_layer": round(chain["norm_in_linear"], 3),
+                                      "separate_norm_kernel_us_per_layer": round(chain["kernels"], 3),
+                                      "reference_structure_us_per_layer": round(chain["reference"], 3)}},
                 "per_call_sweep": {"ms_per_step": round(pms, 5), "gbs": round(pval, 2),
                                    "frac_of_hbm_peak": round(pval / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": pbytes, "launches_per_step": plaunch},

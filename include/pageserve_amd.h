@@ -222,6 +222,35 @@ int pgs_w8a16_swiglu(const void* x, const int8_t* qp_gate, const float* s_gate,
                      size_t workspace_bytes, void* stream);
 
 /*
+ * Replaces h = rms_norm(x, weight, eps) followed by the q/k/v projections of
+ * h -- engine/model.py:166 (rms_norm at :29-34) and :168-170 -- with one
+ * launch where the plan allows (m <= 4 tokens, K % 64 == 0, no K split, bf16
+ * outputs, 16-byte aligned norm weight): the kernel normalises the
+ * activations it stages, with the reference's roundings
+ * (h = bf16(weight * bf16(x * r)), r = 1/sqrt(mean(x^2) + eps) in fp32);
+ * otherwise pgs_rmsnorm into the workspace, then pgs_w8a16_linear_group.
+ * The fp32 sum of squares is formed in a fixed order (deterministic) that
+ * differs from pgs_rmsnorm's, so h may differ from it in the last bf16 bit.
+ * workspace: pgs_w8a16_rmsnorm_workspace_bytes() bytes.
+ */
+int pgs_w8a16_rmsnorm_linear_group(const void* x, const void* norm_weight, float eps,
+                                   const pgs_linear_out* outs, int n_outs, int y_dtype,
+                                   int64_t m, int64_t k, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/*
+ * Replaces h = rms_norm(x, weight, eps); silu(F.linear(h, Wg)) * F.linear(h,
+ * Wu) -- engine/model.py:187-189 -- with one launch where the plan allows
+ * (same conditions and roundings as pgs_w8a16_rmsnorm_linear_group),
+ * otherwise pgs_rmsnorm into the workspace, then pgs_w8a16_swiglu.
+ */
+int pgs_w8a16_rmsnorm_swiglu(const void* x, const void* norm_weight, float eps,
+                             const int8_t* qp_gate, const float* s_gate,
+                             const int8_t* qp_up, const float* s_up, void* act,
+                             int64_t m, int64_t n, int64_t k, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes a linear call needs (0 = none): n[0..n_outs-1] are the
  * out_features of its members (one member for pgs_w8a16_linear; for
  * pgs_w8a16_swiglu pass swiglu = 1 and n[0] = intermediate size).  The value
@@ -230,6 +259,17 @@ int pgs_w8a16_swiglu(const void* x, const int8_t* qp_gate, const float* s_gate,
  */
 size_t pgs_w8a16_workspace_bytes(int64_t m, const int64_t* n, int n_outs,
                                  int64_t k, int swiglu);
+
+/*
+ * Workspace bytes of pgs_w8a16_rmsnorm_linear_group / pgs_w8a16_rmsnorm_swiglu
+ * (same arguments as pgs_w8a16_workspace_bytes): always room for the
+ * normalised activations ([m, k] bf16, used when the norm cannot run inside
+ * the linear kernel) after the linear's own workspace and after the pair
+ * slots at its start (kept empty for later calls sharing the workspace).  No
+ * counterpart in the reference.
+ */
+size_t pgs_w8a16_rmsnorm_workspace_bytes(int64_t m, const int64_t* n, int n_outs,
+                                         int64_t k, int swiglu);
 
 #ifdef __cplusplus
 }

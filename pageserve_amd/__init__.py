@@ -16,6 +16,9 @@ from .quantization import (  # noqa: F401
     mlp,
     quantize_per_channel,
     rmsnorm,
+    rmsnorm_linear_group,
+    rmsnorm_mlp,
+    rmsnorm_swiglu,
     rope_qk,
     save_quantized,
     swiglu,

@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class NativeLibraryError(RuntimeError):
@@ -66,6 +66,11 @@ SIGNATURES = {
     "pgs_rope": (_INT, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _VP, _I64, _I64, _VP]),
     "pgs_w8a16_swiglu": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_w8a16_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
+    "pgs_w8a16_rmsnorm_linear_group": (_INT, [_VP, _VP, ctypes.c_float, ctypes.POINTER(LinearOut), _INT, _INT,
+                                              _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_rmsnorm_swiglu": (_INT, [_VP, _VP, ctypes.c_float, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP,
+                                        _SZ, _VP]),
+    "pgs_w8a16_rmsnorm_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
 }
 
 _lock = threading.Lock()

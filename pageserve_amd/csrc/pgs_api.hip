@@ -28,7 +28,7 @@ int check_launch(const char* what) {
 
 extern "C" {
 
-int pgs_abi_version(void) { return 5; }
+int pgs_abi_version(void) { return 6; }
 
 const char* pgs_error_string(int code) {
   switch (code) {

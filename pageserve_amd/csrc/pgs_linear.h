@@ -33,6 +33,8 @@ struct Problem {
   float* partials;  // split-K partial tiles (null: no split)
   size_t partial_bytes;
   unsigned long long* pairs;  // zeroed pair slots (skinny two-way split), or null
+  const uint16_t* norm_w;     // rms_norm weight fused in front of the linear (bf16 [k]), or null
+  float eps;
 };
 
 // Largest in_features of the linear kernels: their buffer offsets
@@ -63,6 +65,9 @@ struct GemmPlan {
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split);
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat);
+// whether the skinny kernel can apply rms_norm to its staged activations
+// (bf16 output, m <= 4, K % 64 == 0, no K split, an issue-once shape)
+bool skinny_norm_fusable(const SkinnyPlan& p, int m, int k, bool out_f32, int nmat);
 int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st);
 
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split);

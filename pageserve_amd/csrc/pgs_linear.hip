@@ -45,10 +45,32 @@ size_t workspace_bytes(const Plan& p, int nmat) {
   return (part || pairs) ? kPairBytes + part : 0;
 }
 
+// Offset of the normalised activations in the workspace of a fused-norm
+// call that cannot normalise inside the linear kernel: after the linear's own
+// workspace, 256-byte aligned, and never inside the pair slots, which a later
+// call on the same workspace expects to find empty even when this call's plan
+// uses none.
+size_t norm_offset(size_t linear_bytes) {
+  return (std::max(linear_bytes, kPairBytes) + 255) & ~static_cast<size_t>(255);
+}
+
 int run(Problem& p, void* workspace, size_t ws_bytes, hipStream_t st) {
   const int members = (p.nmat == 2) ? 1 : p.args.n_outs;
   const Plan plan = make_plan(p.m, p.k, p.nmat, p.args.n, members, workspace != nullptr);
   const size_t need = workspace_bytes(plan, p.nmat);
+  if (p.norm_w && !(plan.skinny && skinny_norm_fusable(plan.sk, p.m, p.k, p.out_f32, p.nmat) && aligned(p.norm_w, 16))) {
+    // rms_norm as its own kernel into the workspace, then the plain linear
+    const size_t off = norm_offset(need), bytes = static_cast<size_t>(p.m) * p.k * 2;
+    if (!workspace || ws_bytes < off + bytes)
+      return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 (rms_norm fused): workspace of %zu bytes, %zu needed", ws_bytes,
+                  off + bytes);
+    void* h = static_cast<char*>(workspace) + off;
+    int rc = pgs_rmsnorm(p.x, p.norm_w, p.eps, h, p.m, p.k, st);
+    if (rc) return rc;
+    p.x = static_cast<const uint16_t*>(h);
+    p.norm_w = nullptr;
+    ws_bytes = off;
+  }
   if (need > ws_bytes)
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16: workspace of %zu bytes is smaller than the %zu this call needs",
                 ws_bytes, need);
@@ -114,12 +136,26 @@ extern "C" size_t pgs_w8a16_workspace_bytes(int64_t m, const int64_t* n, int n_o
   return workspace_bytes(make_plan(static_cast<int>(m), static_cast<int>(k), nmat, nn, members, true), nmat);
 }
 
+extern "C" size_t pgs_w8a16_rmsnorm_workspace_bytes(int64_t m, const int64_t* n, int n_outs, int64_t k, int swiglu) {
+  if (m <= 0 || k <= 0 || m > 0x7fffffff || k > 0x7fffffff) return 0;
+  const size_t linear = pgs_w8a16_workspace_bytes(m, n, n_outs, k, swiglu);
+  return norm_offset(linear) + static_cast<size_t>(m) * static_cast<size_t>(k) * 2;
+}
+
 namespace {
 
 // q/k/v-style group of linears on the same activations; res (null or one
 // bf16 [m, n] residual per output) is added in the epilogue.
+int check_norm(const char* fn, const void* w, float eps, int64_t m, int64_t k) {
+  if (m > 0 && k > 0 && !w) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null norm weight", fn);
+  if (!aligned(w, 2)) return fail(PGS_ERR_MISALIGNED, "%s: norm weight misaligned", fn);
+  if (!(eps >= 0.f)) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: eps must be >= 0", fn);
+  return PGS_OK;
+}
+
 int linear_group_impl(const char* fn, const void* x, const pgs_linear_out* outs, const void* const* res, int n_outs,
-                      int y_dtype, int64_t m, int64_t k, void* workspace, size_t workspace_bytes_, void* stream) {
+                      int y_dtype, int64_t m, int64_t k, void* workspace, size_t workspace_bytes_, void* stream,
+                      const void* norm_w = nullptr, float eps = 0.f) {
   int rc = check_common(fn, x, m, k);
   if (rc) return rc;
   if (!outs || n_outs < 1 || n_outs > PGS_MAX_GROUP)
@@ -132,6 +168,8 @@ int linear_group_impl(const char* fn, const void* x, const pgs_linear_out* outs,
   p.k = static_cast<int>(k);
   p.nmat = 1;
   p.out_f32 = (y_dtype == PGS_DTYPE_F32);
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
   int used = 0;
   for (int i = 0; i < n_outs; ++i) {
     rc = check_member(fn, outs[i].qp, outs[i].scale, outs[i].bias, outs[i].y, outs[i].n, m, k);
@@ -187,10 +225,11 @@ extern "C" int pgs_w8a16_linear_residual(const void* x, const int8_t* q, const f
                            stream);
 }
 
-extern "C" int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float* s_gate, const int8_t* q_up,
-                                const float* s_up, void* act, int64_t m, int64_t n, int64_t k, void* workspace,
-                                size_t workspace_bytes_, void* stream) {
-  const char* fn = "pgs_w8a16_swiglu";
+namespace {
+
+int swiglu_impl(const char* fn, const void* x, const int8_t* q_gate, const float* s_gate, const int8_t* q_up,
+                const float* s_up, void* act, int64_t m, int64_t n, int64_t k, void* workspace,
+                size_t workspace_bytes_, void* stream, const void* norm_w, float eps) {
   int rc = check_common(fn, x, m, k);
   if (rc) return rc;
   rc = check_member(fn, q_gate, s_gate, nullptr, act, n, m, k);
@@ -217,5 +256,37 @@ extern "C" int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float
   p.args.scale[1] = s_up;
   p.args.n[0] = static_cast<int32_t>(n);
   p.args.n[1] = static_cast<int32_t>(n);
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
   return run(p, workspace, workspace_bytes_, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int pgs_w8a16_swiglu(const void* x, const int8_t* q_gate, const float* s_gate, const int8_t* q_up,
+                                const float* s_up, void* act, int64_t m, int64_t n, int64_t k, void* workspace,
+                                size_t workspace_bytes_, void* stream) {
+  return swiglu_impl("pgs_w8a16_swiglu", x, q_gate, s_gate, q_up, s_up, act, m, n, k, workspace, workspace_bytes_,
+                     stream, nullptr, 0.f);
+}
+
+extern "C" int pgs_w8a16_rmsnorm_linear_group(const void* x, const void* norm_weight, float eps,
+                                              const pgs_linear_out* outs, int n_outs, int y_dtype, int64_t m,
+                                              int64_t k, void* workspace, size_t workspace_bytes_, void* stream) {
+  const char* fn = "pgs_w8a16_rmsnorm_linear_group";
+  int rc = check_norm(fn, norm_weight, eps, m, k);
+  if (rc) return rc;
+  return linear_group_impl(fn, x, outs, nullptr, n_outs, y_dtype, m, k, workspace, workspace_bytes_, stream,
+                           norm_weight, eps);
+}
+
+extern "C" int pgs_w8a16_rmsnorm_swiglu(const void* x, const void* norm_weight, float eps, const int8_t* q_gate,
+                                        const float* s_gate, const int8_t* q_up, const float* s_up, void* act,
+                                        int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes_,
+                                        void* stream) {
+  const char* fn = "pgs_w8a16_rmsnorm_swiglu";
+  int rc = check_norm(fn, norm_weight, eps, m, k);
+  if (rc) return rc;
+  return swiglu_impl(fn, x, q_gate, s_gate, q_up, s_up, act, m, n, k, workspace, workspace_bytes_, stream,
+                     norm_weight, eps);
 }

@@ -90,15 +90,27 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 // <= 80 registers.
 constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
 
+// LDS of a kernel with xm staged tokens (slots of s chunks; the fused norm
+// adds its per-wave partial sums); at most 160 KiB per workgroup on gfx950.
+constexpr int kLdsLimit = 160 * 1024;
+constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, bool norm) {
+  return (xm > 0 ? nw * nb * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
+}
+
 // FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
 // rows 8h .. 8h+7 of tile t.  XM > 0: up to XM tokens (M <= XM, NB > 0, K %
-// 64 == 0, folded), their activations staged through LDS (below).
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM>
+// 64 == 0; folded, or NORM), their activations staged through LDS (below).
+// NORM: the activations are the rows of x after rms_norm with weight nw and
+// eps (engine/model.py:29-34), computed on the staged pieces (splits == 1:
+// the workgroup holds whole rows).
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM, bool NORM>
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
-                                                         unsigned long long* __restrict__ pairs) {
+                                                         unsigned long long* __restrict__ pairs,
+                                                         const uint16_t* __restrict__ nw, float eps) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
-  static_assert(XM == 0 || (NB > 0 && K64 && FOLD), "activation staging covers folded issue-once shapes");
+  static_assert(XM == 0 || (NB > 0 && K64 && (FOLD || NORM)), "activation staging covers folded issue-once shapes");
+  static_assert(!NORM || (XM > 0 && !OUT_F32), "the fused norm works on staged activations");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   // (folded: the two halves of a tile run back to back on one XCD)
@@ -239,8 +251,10 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   if constexpr (NB > 0) {
     Batch bt[NB];
     u32x4 xpiece[XM > 0 ? XPASS : 1];
+    u32x4 wpiece[NORM ? XPASS : 1];  // NORM: the norm weights of the same columns
     if constexpr (XM > 0) {
       // the pieces first, so that parking them waits for them alone
+      const __amdgpu_buffer_rsrc_t nres = make_rsrc(NORM ? nw : x, NORM ? static_cast<int64_t>(K) * 2 : 0);
 #pragma unroll
       for (int i = 0; i < XPASS; ++i) {
         const int p = lane + 64 * i;
@@ -249,9 +263,15 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
         const int t = (p >> 3) % XM, cr = p / (8 * XM);
         const int sw = cr / S;
         const int ch = cb + (first + (sw / U) * kStep + sw % U) * S + cr % S;
-        // (pieces past XP, tokens past M and chunks past K read zeros)
-        const int off = p < XP ? t * K * 2 + ch * 128 + (p & 7) * 16 : 0x7ffffff0;
+        // (pieces past XP, chunks past the range and tokens past M read
+        // zeros: an offset past the buffer; a chunk past K of token t would
+        // otherwise be the start of token t + 1, which the sum of squares
+        // must not see)
+        const bool in = p < XP && ch < ce;
+        const int off = in ? t * K * 2 + ch * 128 + (p & 7) * 16 : 0x7ffffff0;
         xpiece[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0);
+        if constexpr (NORM)
+          wpiece[i] = __builtin_amdgcn_raw_buffer_load_b128(nres, in ? ch * 128 + (p & 7) * 16 : 0x7ffffff0, 0, 0);
       }
 #pragma unroll
       for (int j = 0; j < NB; ++j) load_w(bt[j], first + j * kStep);
@@ -261,6 +281,48 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     }
     epi = load_epi();  // behind the weight loads
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+    if constexpr (NORM) {
+      // rms_norm on the staged pieces.  All pieces of a lane belong to token
+      // (lane / 8) % XM (XM divides 8).  Sum of squares in a fixed order:
+      // each lane over its pieces, the lanes of a token by a butterfly, the
+      // waves in order through LDS; then r = 1 / sqrt(mean + eps) and
+      // h = bf16(w * bf16(x * r)), the reference's roundings.
+      const int tl = (lane >> 3) % XM;
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < XPASS; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16_bits_to_f32(static_cast<uint16_t>(xpiece[i][e]));
+          const float hi = bf16_bits_to_f32(static_cast<uint16_t>(xpiece[i][e] >> 16));
+          ss += lo * lo;
+          ss += hi * hi;
+        }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1)
+        if ((off >> 3) % XM == 0 || off < 8) ss += __shfl_xor(ss, off);  // lanes of the same token
+      __shared__ float npart[NW][XM];
+      if ((lane & ~(8 * XM - 1) & ~7) == 0 && (lane & 7) == 0) npart[wave][tl] = ss;
+      __syncthreads();
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) tot += npart[w][tl];
+      const float r = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+#pragma unroll
+      for (int i = 0; i < XPASS; ++i) {
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = bf16_bits_to_f32(static_cast<uint16_t>(xpiece[i][e]));
+          const float x1 = bf16_bits_to_f32(static_cast<uint16_t>(xpiece[i][e] >> 16));
+          const float g0 = bf16_bits_to_f32(static_cast<uint16_t>(wpiece[i][e]));
+          const float g1 = bf16_bits_to_f32(static_cast<uint16_t>(wpiece[i][e] >> 16));
+          o[e] = pack_bf16x2(g0 * bf16_bits_to_f32(f32_to_bf16_bits(x0 * r)),
+                             g1 * bf16_bits_to_f32(f32_to_bf16_bits(x1 * r)));
+        }
+        xpiece[i] = tl < M ? o : u32x4{0u, 0u, 0u, 0u};  // (tokens past M: never read)
+      }
+    }
     if constexpr (XM > 0) {
 #pragma unroll
       for (int i = 0; i < XPASS; ++i) {
@@ -363,31 +425,38 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * (FOLD ? 2 : plan.splits);
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
   const dim3 g(static_cast<unsigned>(grid)), b(64 * NW);
-  // Up to four tokens in a folded launch stage their activations through
-  // LDS (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 ->
-  // 3.38, o_proj 2.97 -> 3.03; the unfolded SwiGLU pair, 4 chunks per wave,
-  // loses: 9.21 -> 9.33 us, so it keeps direct loads).
-  if constexpr (NB > 0 && FOLD) {
-    if (p.k % 64 == 0 && p.m <= 4) {
-      if (p.m == 1)
-        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1>), g, b, 0, st, p.x, p.args, p.m,
-                           p.k, plan.splits, p.partials, pairs);
-      else if (p.m == 2)
-        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2>), g, b, 0, st, p.x, p.args, p.m,
-                           p.k, plan.splits, p.partials, pairs);
-      else
-        hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4>), g, b, 0, st, p.x, p.args, p.m,
-                           p.k, plan.splits, p.partials, pairs);
-      return check_launch("w8a16 skinny kernel");
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, g, b, 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs, p.norm_w, p.eps);
+    return check_launch("w8a16 skinny kernel");
+  };
+  if constexpr (NB > 0 && !OUT_F32) {
+    // rms_norm applied to the staged activations
+    if (p.norm_w) {
+      if (p.k % 64 != 0 || p.m > 4 || plan.splits != 1 || plan.pair)
+        return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm needs m <= 4 and one K range");
+      constexpr int S = FOLD ? 2 : 1;
+      if (p.m == 1) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, true>);
+      if (p.m == 2) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, true>);
+      if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, S, 4, true) <= kLdsLimit)
+        return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, true>);
+      return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm's staging exceeds LDS");
     }
   }
-  if (p.k % 64 == 0)
-    hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0>), g, b, 0, st, p.x, p.args, p.m,
-                       p.k, plan.splits, p.partials, pairs);
-  else
-    hipLaunchKernelGGL((skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, 0>), g, b, 0, st, p.x, p.args, p.m,
-                       p.k, plan.splits, p.partials, pairs);
-  return check_launch("w8a16 skinny kernel");
+  if (p.norm_w) return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm needs a bf16 output");
+  // Up to four tokens in a folded launch stage their activations through
+  // LDS (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 ->
+  // 3.38, o_proj 2.97 -> 3.03; at four tokens down_proj 7.24 -> 6.85; the
+  // unfolded SwiGLU pair, 4 chunks per wave, loses: 9.21 -> 9.33 us at one
+  // token, so it keeps direct loads).
+  if constexpr (NB > 0 && FOLD) {
+    if (p.k % 64 == 0 && p.m <= 4) {
+      if (p.m == 1) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, false>);
+      if (p.m == 2) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, false>);
+      return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, false>);
+    }
+  }
+  if (p.k % 64 == 0) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0, false>);
+  return go(skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, 0, false>);
 }
 
 template <int NW, int U, int NB, int NMAT, bool OUT_F32>
@@ -474,6 +543,13 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
     if (sh.nw * sh.u * sh.nb >= per_wg) p.shape = i;
   }
   return p;
+}
+
+bool skinny_norm_fusable(const SkinnyPlan& p, int m, int k, bool out_f32, int nmat) {
+  if (out_f32 || m < 1 || m > 4 || k % 64 != 0 || p.splits != 1 || p.pair || p.shape == kLoopShape) return false;
+  const SkinnyShape& sh = kSkinnyShapes[p.shape];
+  return sh.nb > 0 && skinny_lds_bytes(sh.nw, sh.u, sh.nb, nmat, p.fold ? 2 : 1, m == 1 ? 1 : m == 2 ? 2 : 4, true) <=
+                          kLdsLimit;
 }
 
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat) {

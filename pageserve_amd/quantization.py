@@ -115,12 +115,13 @@ _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _ws_need: dict[tuple, int] = {}
 
 
-def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, swiglu: bool):
-    key = (m, ns, k, swiglu)
+def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, swiglu: bool, norm: bool = False):
+    key = (m, ns, k, swiglu, norm)
     need = _ws_need.get(key)
     if need is None:
         arr = (ctypes.c_int64 * len(ns))(*ns)
-        need = int(lib.pgs_w8a16_workspace_bytes(m, arr, len(ns), k, int(swiglu)))
+        query = lib.pgs_w8a16_rmsnorm_workspace_bytes if norm else lib.pgs_w8a16_workspace_bytes
+        need = int(query(m, arr, len(ns), k, int(swiglu)))
         _ws_need[key] = need
     if need == 0:
         return ctypes.c_void_p(0), 0
@@ -430,6 +431,27 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
                  out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
     """Several projections of the same input in one launch (q/k/v,
     engine/model.py:168-170).  Returns one output per weight."""
+    return _linear_group(x, weights, biases, out_dtype, None, 0.0)
+
+
+def rmsnorm_linear_group(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weights: list["QuantizedWeight"],
+                         biases: list | None = None, out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
+    """``h = rms_norm(x, norm_weight, eps)`` then the projections of ``h``
+    (engine/model.py:166-170), in one launch for up to 4 tokens (the kernel
+    normalises the activations it stages; its fixed-order sum of squares may
+    make ``h`` differ from :func:`rmsnorm` in the last bf16 bit), otherwise
+    :func:`rmsnorm` then :func:`linear_group`."""
+    return _linear_group(x, weights, biases, out_dtype, norm_weight, eps)
+
+
+def _norm_weight(w: torch.Tensor, k: int, dev: torch.device, what: str) -> torch.Tensor:
+    if not isinstance(w, torch.Tensor) or w.dtype != torch.bfloat16 or w.numel() != k or w.device != dev:
+        raise ValueError(f"{what}: norm weight must be a bf16 [{k}] tensor on {dev}")
+    w = w.reshape(k)
+    return w if w.is_contiguous() and w.data_ptr() % 16 == 0 else _aligned(w)
+
+
+def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch.Tensor]:
     if not weights or len(weights) > _native.MAX_GROUP:
         raise ValueError(f"linear_group takes 1..{_native.MAX_GROUP} weights")
     biases = list(biases) if biases is not None else [None] * len(weights)
@@ -448,6 +470,7 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
     lead = x.shape[:-1]
     x2 = _check_x(x, k, dev, "linear")
     m = x2.shape[0]
+    nw = _norm_weight(norm_weight, k, dev, "rmsnorm_linear_group") if norm_weight is not None else None
     lib = _native.load()
     outs = (LinearOut * len(weights))()
     ys, keep = [], []
@@ -465,9 +488,14 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
         ys.append(y)
     with _on_device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        ws, ws_bytes = _workspace(lib, dev, stream, m, tuple(w.shape[0] for w in weights), k, False)
-        rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
-                                        ctypes.c_void_p(stream))
+        ws, ws_bytes = _workspace(lib, dev, stream, m, tuple(w.shape[0] for w in weights), k, False, nw is not None)
+        if nw is None:
+            rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
+                                            ctypes.c_void_p(stream))
+        else:
+            rc = lib.pgs_w8a16_rmsnorm_linear_group(_ptr(x2), _ptr(nw), ctypes.c_float(eps), outs, len(weights),
+                                                    _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
+                                                    ctypes.c_void_p(stream))
     check(rc, "w8a16 linear")
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
@@ -475,6 +503,18 @@ def linear_group(x: torch.Tensor, weights: list["QuantizedWeight"], biases: list
 def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> torch.Tensor:
     """``F.silu(F.linear(x, gate)) * F.linear(x, up)`` in one launch
     (engine/model.py:188-190); fp32 inside, one rounding to bf16."""
+    return _swiglu(x, gate, up, None, 0.0)
+
+
+def rmsnorm_swiglu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, gate: "QuantizedWeight",
+                   up: "QuantizedWeight") -> torch.Tensor:
+    """``h = rms_norm(x, norm_weight, eps)`` then :func:`swiglu` of ``h``
+    (engine/model.py:187-189), in one launch for up to 4 tokens (as
+    :func:`rmsnorm_linear_group`)."""
+    return _swiglu(x, gate, up, norm_weight, eps)
+
+
+def _swiglu(x, gate, up, norm_weight, eps) -> torch.Tensor:
     dev = gate.device
     if dev.type != "cuda" or up.device != dev:
         raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
@@ -487,12 +527,17 @@ def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> t
     act = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     qg, sg = gate._kernel_operands()
     qu, su = up._kernel_operands()
+    nw = _norm_weight(norm_weight, k, dev, "rmsnorm_swiglu") if norm_weight is not None else None
     lib = _native.load()
     with _on_device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, True)
-        rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, ws, ws_bytes,
-                                  ctypes.c_void_p(stream))
+        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, True, nw is not None)
+        if nw is None:
+            rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, ws,
+                                      ws_bytes, ctypes.c_void_p(stream))
+        else:
+            rc = lib.pgs_w8a16_rmsnorm_swiglu(_ptr(x2), _ptr(nw), ctypes.c_float(eps), _ptr(qg), _ptr(sg), _ptr(qu),
+                                              _ptr(su), _ptr(act), m, n, k, ws, ws_bytes, ctypes.c_void_p(stream))
     check(rc, "w8a16 swiglu")
     return act.reshape(*lead, n)
 
@@ -503,6 +548,14 @@ def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "
     fused gate/up kernel, then the down projection; with ``residual`` the
     add of engine/model.py:190 runs in the down projection's epilogue."""
     return linear(swiglu(x, gate, up), down, residual=residual)
+
+
+def rmsnorm_mlp(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, gate: "QuantizedWeight",
+                up: "QuantizedWeight", down: "QuantizedWeight", residual: torch.Tensor | None = None) -> torch.Tensor:
+    """engine/model.py:187-190: ``rms_norm`` and the fused gate/up kernel in
+    one launch (:func:`rmsnorm_swiglu`), then the down projection with the
+    optional residual add in its epilogue."""
+    return linear(rmsnorm_swiglu(x, norm_weight, eps, gate, up), down, residual=residual)
 
 
 # ---------------------------------------------------------------------------

@@ -53,6 +53,16 @@ def test_abi_version_and_error_strings(native_lib):
         (lambda L: L.pgs_unpack_weight(ctypes.c_void_p(8), 4, 64, ctypes.c_void_p(16), None), b"aligned"),
         (lambda L: L.pgs_dequantize_packed(None, None, -1, 64, None, 0, None), b"negative size"),
         (lambda L: L.pgs_quantize_per_channel_packed(None, 3, 4, 64, None, None, None), b"dtype"),
+        (lambda L: L.pgs_w8a16_rmsnorm_linear_group(None, None, 1e-6, None, 1, 1, 1, 64, None, 0, None),
+         b"null norm weight"),
+        (lambda L: L.pgs_w8a16_rmsnorm_linear_group(None, ctypes.c_void_p(17), 1e-6, None, 1, 1, 1, 64, None, 0,
+                                                    None), b"norm weight misaligned"),
+        (lambda L: L.pgs_w8a16_rmsnorm_swiglu(None, ctypes.c_void_p(16), -1.0, None, None, None, None, None, 1, 16,
+                                              64, None, 0, None), b"eps"),
+        (lambda L: L.pgs_w8a16_rmsnorm_swiglu(None, ctypes.c_void_p(16), float("nan"), None, None, None, None, None,
+                                              1, 16, 64, None, 0, None), b"eps"),
+        (lambda L: L.pgs_w8a16_rmsnorm_linear_group(ctypes.c_void_p(16), ctypes.c_void_p(16), 1e-6, None, 0, 1, 1,
+                                                    64, None, 0, None), b"n_outs"),
     ],
 )
 def test_bad_arguments_are_rejected_without_launching(native_lib, call, needle):
@@ -94,6 +104,23 @@ def test_workspace_query(native_lib):
     assert need(1, [0], 2048) == 0
     assert need(12, [1024, 256, 256], 2048) >= need(12, [2048], 2048) > 0   # o / a small q|k|v group
     assert need(8, [1024, 256, 256], 2048) == 0                 # folded
+
+
+def test_rmsnorm_workspace_query(native_lib):
+    """The fused-norm calls need room for h = rms_norm(x) (m x k bf16) past
+    the linear's own workspace, for the cases that cannot normalise inside
+    the projection kernel."""
+    def need(fn, m, ns, k, swiglu=0):
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        return fn(m, arr, len(ns), k, swiglu)
+
+    for m, ns, k, sw in [(1, [2048, 256, 256], 2048, 0), (16, [2048], 11008, 0), (512, [11008], 2048, 1),
+                         (3, [1104], 640, 0)]:
+        base = need(native_lib.pgs_w8a16_workspace_bytes, m, ns, k, sw)
+        fused = need(native_lib.pgs_w8a16_rmsnorm_workspace_bytes, m, ns, k, sw)
+        # h lies past the linear's workspace and past the pair slots (256 x 256 x 8 bytes at its start)
+        assert fused - m * k * 2 >= max(base, 256 * 256 * 8) and fused - m * k * 2 < max(base, 256 * 256 * 8) + 256
+    assert need(native_lib.pgs_w8a16_rmsnorm_workspace_bytes, 0, [2048], 2048) == 0
 
 
 @pytest.mark.parametrize("n,k,expect", [(16, 64, 1024), (17, 64, 2048), (16, 65, 2048), (0, 64, 0), (2048, 11008,
