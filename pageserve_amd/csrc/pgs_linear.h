@@ -43,16 +43,18 @@ constexpr int kMaxK = 1 << 22;
 
 // Workspace layout: kPairBytes of pair slots (zero before first use, left
 // zero by every call), then the split-K partial tiles.  One 8-byte slot per
-// output of a 16-row tile: 256 tiles x 16 rows x 16 tokens.
+// output of a 16-row tile: 256 tiles x 16 rows x 16 tokens (128 tiles at up
+// to 32 tokens).
 constexpr size_t kPairBytes = 256u * 256u * 8u;
 
-// Launch plan of the skinny kernel (m <= 16).
+// Launch plan of the skinny kernel (m <= 32).
 struct SkinnyPlan {
   int tiles;   // 16-row tiles over all members
   int splits;  // workgroups per tile (split K across workgroups)
   bool pair;   // two K halves combined through pair slots (no reduce launch)
   int shape;   // launch shape: waves per workgroup and K slots per wave
   bool fold;   // two workgroups of 8 rows per tile, two chunks per MFMA (m <= 8)
+  int tm;      // 16-token column blocks per tile (1: m <= 16, 2: m <= 32)
 };
 
 // Launch plan of the tile GEMM (m > 16).

@@ -12,7 +12,7 @@
 namespace pgs {
 namespace {
 
-constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyMaxM = 32;
 
 struct Plan {
   bool skinny;

@@ -1,4 +1,4 @@
-// Skinny W8A16 kernel for decode-sized inputs (m <= 16 tokens).
+// Skinny W8A16 kernel for decode-sized inputs (m <= 32 tokens).
 //
 // Memory bound: every int8 weight byte is read from HBM exactly once, from
 // the packed tile layout (pgs_common.h) with 128-bit non-temporal loads, so
@@ -23,7 +23,11 @@
 // so that output (token t, row r) is C[r][t] + C[r+8][t+m].  Each lane's
 // 16 bytes are still one contiguous piece of the packed block, the
 // instruction stream equals that of a K split, and nothing crosses
-// workgroups.  Results never depend on timing: every sum has a fixed order.
+// workgroups.  17..32 tokens use two 16-token column blocks (TM = 2): each
+// widened weight fragment feeds one MFMA per block, and every wave still
+// issues its loads at once with no barrier inside its K range (a tiled GEMM
+// with activations shared through LDS synchronises its waves at every K
+// step).  Results never depend on timing: every sum has a fixed order.
 #include "pgs_linear.h"
 
 namespace pgs {
@@ -88,7 +92,9 @@ __device__ __forceinline__ void epilogue(const GroupArgs& a, int g, int n, int m
 // 8 waves x 2 batches holds 64 registers of loads per lane, and three of its
 // workgroups per CU (all 688 of a 2048 x 11008 pair resident at once) need
 // <= 80 registers.
-constexpr int skinny_occ(int nw, int nb, int nmat) { return (nmat == 2 && nw == 8 && nb == 2) ? 6 : 1; }
+constexpr int skinny_occ(int nw, int nb, int nmat, int tm) {
+  return (tm == 1 && nmat == 2 && nw == 8 && nb == 2) ? 6 : 1;
+}
 
 // LDS of a kernel with xm staged tokens (slots of s chunks; the fused norm
 // adds its per-wave partial sums); at most 160 KiB per workgroup on gfx950.
@@ -102,15 +108,16 @@ constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, b
 // 64 == 0; folded, or NORM), their activations staged through LDS (below).
 // NORM: the activations are the rows of x after rms_norm with weight nw and
 // eps (engine/model.py:29-34), computed on the staged pieces (splits == 1:
-// the workgroup holds whole rows).
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM, bool NORM>
-__global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
+// the workgroup holds whole rows).  TM: 16-token column blocks (M <= 16 TM).
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM, bool NORM, int TM = 1>
+__global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs,
                                                          const uint16_t* __restrict__ nw, float eps) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
   static_assert(XM == 0 || (NB > 0 && K64 && (FOLD || NORM)), "activation staging covers folded issue-once shapes");
   static_assert(!NORM || (XM > 0 && !OUT_F32), "the fused norm works on staged activations");
+  static_assert(TM == 1 || (TM == 2 && !FOLD && XM == 0), "two token blocks: unfolded, direct activation loads");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   // (folded: the two halves of a tile run back to back on one XCD)
@@ -125,8 +132,8 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   const int lrow = lane & 15;
   const int kgrp = lane >> 4;
 
-  // one output per thread (M * 16 <= 256 <= 64 * NW): token mm, tile row oi
-  static_assert(NW >= 4, "the epilogue gives each thread at most one output");
+  // one output per thread (M * 16 <= 256 TM <= 64 * NW): token mm, tile row oi
+  static_assert(NW >= 4 && 64 * NW >= 256 * TM, "the epilogue gives each thread at most one output");
   const int idx = threadIdx.x;
   const int mm = FOLD ? idx >> 3 : idx >> 4;
   const int oi = FOLD ? 8 * half + (idx & 7) : idx & 15;
@@ -162,10 +169,12 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   const int xrow = FOLD ? (lrow < M ? lrow : (xsub ? lrow - M : 0)) : min(lrow, M - 1);
   const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<int64_t>(M) * K * 2);
   const int xoff = xrow * K * 2 + xsub * 128 + kgrp * 32;
+  // (TM = 2) B operand column lrow of the second block: token min(16 + lrow, M - 1)
+  const int xoff2 = min(16 + lrow, M - 1) * K * 2 + kgrp * 32;
 
-  f32x4 acc[NMAT];
+  f32x4 acc[NMAT], acc2[NMAT];  // acc2: second token block (TM = 2)
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat) acc[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mat = 0; mat < NMAT; ++mat) acc[mat] = acc2[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto mac = [&](const u32x4 (&wv)[NMAT], u32x4 x0, u32x4 x1) {
     const bf16x8 b0 = __builtin_bit_cast(bf16x8, x0);
@@ -174,6 +183,18 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     for (int mat = 0; mat < NMAT; ++mat) {
       acc[mat] = mfma16x16x32(i8x8_to_bf16x8(wv[mat][0], wv[mat][1]), b0, acc[mat]);
       acc[mat] = mfma16x16x32(i8x8_to_bf16x8(wv[mat][2], wv[mat][3]), b1, acc[mat]);
+    }
+  };
+  // both token blocks: each weight fragment widened once, used twice
+  auto mac2 = [&](const u32x4 (&wv)[NMAT], u32x4 x0, u32x4 x1, u32x4 y0, u32x4 y1) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      const bf16x8 w0 = i8x8_to_bf16x8(wv[mat][0], wv[mat][1]);
+      const bf16x8 w1 = i8x8_to_bf16x8(wv[mat][2], wv[mat][3]);
+      acc[mat] = mfma16x16x32(w0, __builtin_bit_cast(bf16x8, x0), acc[mat]);
+      acc[mat] = mfma16x16x32(w1, __builtin_bit_cast(bf16x8, x1), acc[mat]);
+      acc2[mat] = mfma16x16x32(w0, __builtin_bit_cast(bf16x8, y0), acc2[mat]);
+      acc2[mat] = mfma16x16x32(w1, __builtin_bit_cast(bf16x8, y1), acc2[mat]);
     }
   };
 
@@ -190,7 +211,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
   // workgroup); NB = 0 (long K): groups of two batches in a loop.
   struct Batch {
     u32x4 w[U][NMAT];
-    u32x4 x[U][2];
+    u32x4 x[U][2 * TM];
   };
   auto load_w = [&](Batch& b, int c) {
 #pragma unroll
@@ -210,6 +231,10 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
       // next row or zeros; mac_batch masks them)
       b.x[u][0] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, (cb + c0) * 128, 0);
       b.x[u][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, (cb + c0) * 128, 0);
+      if constexpr (TM == 2) {
+        b.x[u][2] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff2, (cb + c0) * 128, 0);
+        b.x[u][3] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff2 + 16, (cb + c0) * 128, 0);
+      }
     }
   };
 
@@ -238,6 +263,8 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
       if constexpr (XM > 0) {
         const u32x4* src = xw + (((j * U + u) * S + xsub) * XM + xrow) * 9 + kgrp * 2;
         mac(b.w[u], src[0] & mask, src[1] & mask);
+      } else if constexpr (TM == 2) {
+        mac2(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask, b.x[u][2] & mask, b.x[u][3] & mask);
       } else {
         mac(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask);
       }
@@ -347,25 +374,29 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     }
   }
 
-  __shared__ f32x4 red[NW][NMAT][64];
+  __shared__ f32x4 red[NW][NMAT * TM][64];
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat) red[wave][mat][lane] = acc[mat];
+  for (int mat = 0; mat < NMAT; ++mat) {
+    red[wave][mat * TM][lane] = acc[mat];
+    if constexpr (TM == 2) red[wave][mat * TM + 1][lane] = acc2[mat];
+  }
   __syncthreads();
 
   if (idx >= nout) return;
-  const int ln = acc_lane(FOLD ? oi & 7 : oi, mm), r = oi & 3;
+  // token mm is column mm % 16 of block mm / 16
+  const int ln = acc_lane(FOLD ? oi & 7 : oi, mm & 15), r = oi & 3, tb = TM == 2 ? mm >> 4 : 0;
   float v[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) t += red[w][mat][ln][r];
+    for (int w = 0; w < NW; ++w) t += red[w][mat * TM + tb][ln][r];
     if constexpr (FOLD) {
       // the second chunk of every slot: C[r + 8][mm + M]
       const int ln2 = acc_lane((oi & 7) + 8, mm + M);
       float t2 = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) t2 += red[w][mat][ln2][r];
+      for (int w = 0; w < NW; ++w) t2 += red[w][mat * TM][ln2][r];
       t += t2;
     }
     v[mat] = t;
@@ -378,7 +409,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
     // does not depend on the arrival order (fp32 addition is commutative).
     // System scope: the two workgroups run on different XCDs, and the
     // exchange is then performed beyond their L2s.
-    unsigned long long* slot = pairs + static_cast<int64_t>(tile) * 256 + idx;
+    unsigned long long* slot = pairs + static_cast<int64_t>(tile) * (256 * TM) + idx;
     const unsigned long long prev = __hip_atomic_exchange(slot, (1ull << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_SYSTEM);
     if (prev >> 32) {
@@ -387,16 +418,16 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT)) void skinny_kern
       if (has_out) epilogue<NMAT, OUT_F32>(a, g, row0 + oi, mm, N, v, epi);
     }
   } else if (splits > 1) {
-    float* mine = partials + (static_cast<int64_t>(tile) * splits + s) * (NMAT * 256);
+    float* mine = partials + (static_cast<int64_t>(tile) * splits + s) * (NMAT * 256 * TM);
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) mine[mat * 256 + idx] = v[mat];
+    for (int mat = 0; mat < NMAT; ++mat) mine[mat * 256 * TM + idx] = v[mat];
   } else if (has_out) {
     epilogue<NMAT, OUT_F32>(a, g, row0 + oi, mm, N, v, epi);
   }
 }
 
 // Sums the split partial tiles of each 16-row tile in split order, then runs
-// the epilogue.  One 256-thread workgroup per tile (<= 16 x 16 outputs).
+// the epilogue.  One 256-thread workgroup per tile (16 rows x up to 32 tokens).
 template <int NMAT, bool OUT_F32>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, int splits,
                                                             const float* __restrict__ partials) {
@@ -404,20 +435,22 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
   const int g = (NMAT == 2) ? 0 : member_of(a, tile);
   const int N = pick_early(a.n, g);
   const int row0 = (tile - pick_early(a.unit_begin, g)) * 16;
-  const int idx = threadIdx.x;
-  if (idx >= M * 16) return;
-  const int mm = idx >> 4, i = idx & 15;
-  if (row0 + i >= N) return;
-  const float* base = partials + static_cast<int64_t>(tile) * splits * (NMAT * 256);
-  float v[NMAT];
+  // outputs per tile and matrix: 16 rows x 16 tokens per 16-token block
+  const int slots = 256 * ((M + 15) >> 4);
+  const float* base = partials + static_cast<int64_t>(tile) * splits * (NMAT * slots);
+  for (int idx = threadIdx.x; idx < M * 16; idx += 256) {
+    const int mm = idx >> 4, i = idx & 15;
+    if (row0 + i >= N) continue;
+    float v[NMAT];
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat) {
-    float t = 0.f;
-    for (int sp = 0; sp < splits; ++sp) t += base[sp * (NMAT * 256) + mat * 256 + idx];
-    v[mat] = t;
+    for (int mat = 0; mat < NMAT; ++mat) {
+      float t = 0.f;
+      for (int sp = 0; sp < splits; ++sp) t += base[(sp * NMAT + mat) * slots + idx];
+      v[mat] = t;
+    }
+    epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v, epilogue_load<NMAT>(a, g, row0 + i, mm, N,
+                                         reinterpret_cast<const uint16_t*>(pick_early(a.scale, g) + row0 + i)));
   }
-  epilogue<NMAT, OUT_F32>(a, g, row0 + i, mm, N, v, epilogue_load<NMAT>(a, g, row0 + i, mm, N,
-                                       reinterpret_cast<const uint16_t*>(pick_early(a.scale, g) + row0 + i)));
 }
 
 template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool FOLD>
@@ -443,6 +476,18 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
     }
   }
   if (p.norm_w) return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm needs a bf16 output");
+  // 17..32 tokens: two token blocks, unfolded, on shapes of >= 8 waves whose
+  // loads fit the registers (two batches per wave, or the looping kernel)
+  if (p.m > 16) {
+    if constexpr (!FOLD && NW >= 8 && (NB == 2 || NB == 0)) {
+      if (p.m > 32 || plan.tm != 2)
+        return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: m=%d with %d token blocks", p.m, plan.tm);
+      if (p.k % 64 == 0) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 0, false, 2>);
+      return go(skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, false, 0, false, 2>);
+    } else {
+      return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: no two-block kernel for this launch shape (m=%d)", p.m);
+    }
+  }
   // Up to four tokens in a folded launch stage their activations through
   // LDS (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 ->
   // 3.38, o_proj 2.97 -> 3.03; at four tokens down_proj 7.24 -> 6.85; the
@@ -482,12 +527,14 @@ int launch_cfg(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
 
 // Launch shapes (waves per workgroup, slots per batch, batches per wave);
 // a workgroup covers NW * U * NB slots of 64 k (128 k folded).  Index
-// kLoopShape: the looping kernel for longer ranges.
+// kLoopShape: the looping kernel for longer ranges; kLoop8Shape: the same
+// with 8 waves, for two token blocks.
 struct SkinnyShape {
   int nw, u, nb;
 };
-constexpr SkinnyShape kSkinnyShapes[] = {{4, 2, 1}, {4, 2, 2}, {8, 2, 2}, {16, 2, 2}, {16, 1, 6}, {16, 2, 4}, {16, 2, 0}};
-constexpr int kLoopShape = 6;
+constexpr SkinnyShape kSkinnyShapes[] = {{4, 2, 1}, {4, 2, 2}, {8, 2, 2},  {16, 2, 2},
+                                         {16, 1, 6}, {16, 2, 4}, {16, 2, 0}, {8, 2, 0}};
+constexpr int kLoopShape = 6, kLoop8Shape = 7;
 
 template <int NMAT, bool OUT_F32>
 int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
@@ -497,6 +544,7 @@ int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
     case 2: return launch_cfg<8, 2, 2, NMAT, OUT_F32>(p, plan, st);
     case 3: return launch_cfg<16, 2, 2, NMAT, OUT_F32>(p, plan, st);
     case 4: return launch_cfg<16, 1, 6, NMAT, OUT_F32>(p, plan, st);
+    case kLoop8Shape: return launch_cfg<8, 2, 0, NMAT, OUT_F32>(p, plan, st);
     case 5:
       if constexpr (NMAT == 1) return launch_cfg<16, 2, 4, NMAT, OUT_F32>(p, plan, st);
       [[fallthrough]];
@@ -521,14 +569,19 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // workgroups when K is long or when at most 128 tiles meet several tokens
   // (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a 32-chunk K is faster
   // unsplit, without the pair slot's round trip (q|k|v at 16 tokens: 4.7 vs
-  // 5.4 us).
-  SkinnyPlan p{tiles, 1, false, kLoopShape, false};
+  // 5.4 us).  17..32 tokens (two token blocks): 8-wave workgroups (16 waves
+  // are slower: o_proj at 32 tokens 6.4 vs 10.2 us), two batches per wave or
+  // the looping kernel (down_proj 15.8 vs 17.5 us with 16 waves), K split in
+  // pairs only for a long K (o_proj unsplit 6.4 vs 7.3 us paired; the slots
+  // hold 128 tiles of 16 x 32 outputs).
+  SkinnyPlan p{tiles, 1, false, kLoopShape, false, m > 16 ? 2 : 1};
   const int chunks = (k + 63) / 64;
   if (nmat == 1 && chunks >= 16 && tiles < 256 && m <= 8 &&
       (m <= 2 || (tiles <= 128 && (m <= 4 || chunks < 64)))) {
     p.fold = true;
   } else if (can_split && tiles < 256) {
-    if (nmat == 1 && chunks >= 16 && (chunks >= 64 || (m > 4 && tiles <= 128))) {
+    if (nmat == 1 && chunks >= 16 && tiles * p.tm <= 256 &&
+        (chunks >= 64 || (m > 4 && p.tm == 1 && tiles <= 128))) {
       p.splits = 2;  // K halves combined through pair slots
       p.pair = true;
     } else if (chunks >= 128) {
@@ -538,6 +591,11 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   const int per_wg = p.fold ? (chunks + 1) / 2 : (chunks + p.splits - 1) / p.splits;
   // (the SwiGLU pair stops at 96 chunks: 128 would not fit its registers)
   const int last = nmat == 2 ? 4 : 5;
+  if (p.tm == 2) {
+    const SkinnyShape& sh = kSkinnyShapes[2];
+    p.shape = sh.nw * sh.u * sh.nb >= per_wg ? 2 : kLoop8Shape;
+    return p;
+  }
   for (int i = last; i >= 0; --i) {
     const SkinnyShape& sh = kSkinnyShapes[i];
     if (sh.nw * sh.u * sh.nb >= per_wg) p.shape = i;
@@ -553,11 +611,13 @@ bool skinny_norm_fusable(const SkinnyPlan& p, int m, int k, bool out_f32, int nm
 }
 
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat) {
-  return (p.splits > 1 && !p.pair) ? static_cast<size_t>(p.tiles) * p.splits * nmat * 256 * sizeof(float) : 0;
+  return (p.splits > 1 && !p.pair) ? static_cast<size_t>(p.tiles) * p.splits * nmat * 256 * p.tm * sizeof(float) : 0;
 }
 
 int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
-  if (plan.pair && (!p.pairs || plan.tiles * 256 * sizeof(unsigned long long) > kPairBytes || p.nmat != 1))
+  if (p.m < 1 || p.m > 16 * plan.tm || plan.tm < 1 || plan.tm > 2)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: m=%d with %d token blocks", p.m, plan.tm);
+  if (plan.pair && (!p.pairs || plan.tiles * 256 * plan.tm * sizeof(unsigned long long) > kPairBytes || p.nmat != 1))
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: paired split without pair slots");
   if (plan.splits > 1 && !plan.pair && (!p.partials || p.partial_bytes < skinny_partial_bytes(plan, p.nmat)))
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: split-K plan without a large enough workspace");

@@ -49,6 +49,10 @@ SHAPES = [
     (8, 2048, 11008),
     # one to four tokens, folded, activations staged through LDS: odd chunk counts
     (1, 2048, 1088), (1, 300, 4160), (2, 2048, 1088), (4, 300, 4160), (3, 130, 2112),
+    # 17..32 tokens, two token blocks: paired o and down_proj (looping), wide
+    # unsplit, K tails, a long K over few tiles
+    (17, 2048, 2048), (24, 2048, 11008), (32, 11008, 2048), (32, 2048, 2048), (25, 1000, 1040),
+    (30, 130, 4160), (19, 4864, 896),
 ]
 
 
@@ -60,14 +64,14 @@ def test_linear_matches_oracle(gpu, m, n, k):
     report(to_np(y), O.linear(x, q, s), k, f"linear m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m", [1, 3, 16, 40, 256])
+@pytest.mark.parametrize("m", [1, 3, 16, 24, 40, 256])
 def test_linear_with_bias(gpu, m):
     qw, q, s, x, b = _problem(gpu, 7 + m, m, 2048, 2048, bias=True)
     y = qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu))
     report(to_np(y), O.linear(x, q, s, b), 2048, f"linear+bias m={m}")
 
 
-@pytest.mark.parametrize("m", [1, 8, 20, 256])
+@pytest.mark.parametrize("m", [1, 8, 20, 32, 256])
 def test_fp32_output(gpu, m):
     qw, q, s, x, _ = _problem(gpu, 50 + m, m, 1536, 2048)
     y = qw.linear(bf16_gpu(x, gpu), out_dtype=torch.float32)
@@ -77,7 +81,7 @@ def test_fp32_output(gpu, m):
     assert r["rel"] < 1e-4
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 64, 512])
+@pytest.mark.parametrize("m", [1, 5, 16, 24, 32, 64, 512])
 def test_grouped_qkv_matches_separate_calls(gpu, m):
     """q/k/v (engine/model.py:168-170) in one launch: each output matches the
     oracle and its single-weight launch within tolerance.  (Not bit for bit:
@@ -135,7 +139,8 @@ def test_paired_split_leaves_the_workspace_clean(gpu):
     slots) and repeat: every result must match the oracle."""
     cases = [_problem(gpu, 300 + j, m, n, k) for j, (m, n, k) in
              enumerate([(1, 2048, 2048), (12, 2048, 11008), (9, 1000, 1040), (16, 256, 2048), (1, 33, 1024),
-                        (16, 2048, 2048), (3, 1000, 1040)])]
+                        (16, 2048, 2048), (3, 1000, 1040), (24, 2048, 11008), (32, 2048, 2048),
+                        (17, 1000, 1040)])]
     xs = [bf16_gpu(c[3], gpu) for c in cases]
     refs = [O.linear(c[3], c[1], c[2]) for c in cases]
     for rep in range(3):
@@ -144,7 +149,8 @@ def test_paired_split_leaves_the_workspace_clean(gpu):
             report(to_np(y), ref, x.shape[1], f"paired m={x.shape[0]} n={q.shape[0]} k={x.shape[1]} rep={rep}")
 
 
-@pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48)])
+@pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48),
+                                   (20, 2048, 2048), (32, 256, 2048), (27, 300, 1040)])
 def test_nonfinite_token_stays_in_its_row(gpu, m, n, k):
     """A token whose activations hold inf and nan poisons only its own
     outputs (as in x @ W^T): padding columns and the K range of another

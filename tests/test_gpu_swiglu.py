@@ -32,7 +32,9 @@ def _mlp_weights(gpu, seed, inter, hidden):
                                             (50, 130, 48), (24, 256, 4112),
                                             # 128-token x 64-row tiles: split K, ragged M and N
                                             (100, 256, 4096), (300, 1000, 2048), (65, 64, 64),
-                                            (33, 1000, 2048)])
+                                            (33, 1000, 2048),
+                                            # two token blocks: unsplit, and a long K split into partials
+                                            (32, 11008, 2048), (24, 1000, 8192), (21, 300, 1040)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
     ws = _mlp_weights(gpu, 10 + m + inter, inter, hidden)
     x = activations(m, m, hidden)

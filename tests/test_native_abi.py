@@ -104,6 +104,11 @@ def test_workspace_query(native_lib):
     assert need(1, [0], 2048) == 0
     assert need(12, [1024, 256, 256], 2048) >= need(12, [2048], 2048) > 0   # o / a small q|k|v group
     assert need(8, [1024, 256, 256], 2048) == 0                 # folded
+    # 17..32 tokens: two 16-token blocks per tile (pair slots for 128 tiles;
+    # partials of 16 x 32 outputs per tile and matrix for the SwiGLU pair)
+    assert need(32, [2048], 11008) == 256 * 256 * 8
+    assert need(24, [1000], 8192, 1) == 256 * 256 * 8 + 63 * 2 * 2 * 512 * 4
+    assert need(16, [1000], 8192, 1) == 256 * 256 * 8 + 63 * 2 * 2 * 256 * 4
 
 
 def test_rmsnorm_workspace_query(native_lib):
