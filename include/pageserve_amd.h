@@ -129,7 +129,7 @@ int pgs_dequantize_packed(const int8_t* qp, const float* scale, int64_t n,
  * at engine/model.py:193.
  *   y[i,r] = sum_j x[i,j] * q[r,j] * scale[r] (+ bias[r]),  fp32 accumulate,
  * with the weight given packed (qp).  The dense weight is never materialised.  y_dtype: PGS_DTYPE_BF16 or
- * PGS_DTYPE_F32.  Dispatches on m: the skinny kernel for m <= 16, the
+ * PGS_DTYPE_F32.  Dispatches on m: the skinny kernel for m <= 32, the
  * MFMA tile kernel above.
  */
 int pgs_w8a16_linear(const void* x, const int8_t* qp, const float* scale,

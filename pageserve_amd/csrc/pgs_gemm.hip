@@ -1,4 +1,4 @@
-// W8A16 MFMA GEMM for prefill-sized inputs (m > 16 tokens).
+// W8A16 MFMA GEMM for prefill-sized inputs (m > 32 tokens).
 //
 // Output tile BM tokens x BN weight rows per workgroup of 4 waves, K stepped
 // 64 at a time (one packed weight block column).  The waves split the tile
@@ -681,12 +681,12 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
     if constexpr (NMAT == 2) {
       // the SwiGLU pair above 128 tokens: 128 tokens x 64 rows per matrix
       // (each widened weight operand feeds 8 MFMAs; B operands are reused
-      // across the pair's two A tiles per wave); 17..128 tokens: 64 x 64
+      // across the pair's two A tiles per wave); 33..128 tokens: 64 x 64
       // tiles in two K groups
       if (plan.bm == 128) return launch_k64<128, 64, 2, OUT_F32, 2, 1, 2>(x, ga, st);
       return launch_k64<64, 64, 2, OUT_F32, 2, 2, 1, 2>(x, ga, st);
     } else {
-      // single matrices at 17..128 tokens: 64-row tiles in four K groups
+      // single matrices at 33..128 tokens: 64-row tiles in four K groups
       return plan.bm == 32 ? launch_k64<32, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st)
                            : launch_k64<64, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
     }
@@ -699,7 +699,7 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split) {
   GemmPlan p{};
   const int kb = (k + kBK - 1) / kBK;
-  // 17..128 tokens (K % 64 == 0): weight streaming dominates, so 64-row
+  // 33..128 tokens (K % 64 == 0): weight streaming dominates, so 64-row
   // tiles and K groups keep more workgroups and more weight bytes in flight
   const bool mid = k % kBK == 0 && m <= 128;
   p.bn = (mid || (nmat == 2 && k % kBK == 0)) ? 64 : kBN;

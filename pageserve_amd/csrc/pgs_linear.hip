@@ -1,5 +1,5 @@
 // C entry points of the W8A16 linear path: argument checks, the launch plan
-// (skinny kernel for m <= 16, tile GEMM above) and the split-K workspace.
+// (skinny kernel for m <= 32, tile GEMM above) and the split-K workspace.
 //
 // Replaces the reference's per-call "dequantize to a dense weight, then GEMM"
 // (engine/quantization.py:26-27 via engine/model.py:25-26 feeding F.linear at

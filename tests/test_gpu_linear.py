@@ -40,7 +40,7 @@ SHAPES = [
     # K below one 64-column block and K tails on the tiled path; a split-K
     # plan (few tiles, long K) whose last block is partial
     (20, 48, 16), (33, 130, 32), (40, 96, 48), (40, 256, 4112), (70, 2048, 11024),
-    # 17..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also split)
+    # 33..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also split)
     (70, 2048, 11008), (128, 2048, 11008), (96, 2560, 2048), (17, 300, 128),
     # folded decode (8-row halves of a tile, two K chunks per MFMA, m <= 8):
     # 2m = 16 columns, an odd chunk count with a K tail, 6 tokens
