@@ -565,7 +565,11 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // paired at one token, 7.2 vs 7.4 at 4, 9.1 vs 8.1 at 8) and 129..255
   // tiles, which fill the CUs unsplit, only at up to 2 (q|k|v at one token:
   // 3.55 vs 3.62 us, at 4: 3.83 vs 3.82); o_proj: 3.0 vs 3.4 us at one token,
-  // 3.4 vs 4.0 at 8.  Past the fold, a single matrix splits K over two
+  // 3.4 vs 4.0 at 8.  With 256 tiles or more (lm_head, a lone gate_proj) a
+  // short K still folds at up to 3 tokens: the halves' two chunks per MFMA
+  // and staged activations beat the unfolded launch (lm_head [151936, 2048]
+  // at one token 47.5 vs 52.0 us, at 3: 50.2 vs 53.2; 11008 x 2048 at one
+  // token 6.0 vs 6.6; even at 4, slower at 8).  Past the fold, a single matrix splits K over two
   // workgroups when K is long or when at most 128 tiles meet several tokens
   // (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a 32-chunk K is faster
   // unsplit, without the pair slot's round trip (q|k|v at 16 tokens: 4.7 vs
@@ -576,8 +580,9 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // hold 128 tiles of 16 x 32 outputs).
   SkinnyPlan p{tiles, 1, false, kLoopShape, false, m > 16 ? 2 : 1};
   const int chunks = (k + 63) / 64;
-  if (nmat == 1 && chunks >= 16 && tiles < 256 && m <= 8 &&
-      (m <= 2 || (tiles <= 128 && (m <= 4 || chunks < 64)))) {
+  if (nmat == 1 && chunks >= 16 && m <= 8 &&
+      ((tiles < 256 && (m <= 2 || (tiles <= 128 && (m <= 4 || chunks < 64)))) ||
+       (tiles >= 256 && m <= 3 && chunks < 64))) {
     p.fold = true;
   } else if (can_split && tiles < 256) {
     if (nmat == 1 && chunks >= 16 && tiles * p.tm <= 256 &&

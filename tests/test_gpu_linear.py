@@ -53,6 +53,8 @@ SHAPES = [
     # unsplit, K tails, a long K over few tiles
     (17, 2048, 2048), (24, 2048, 11008), (32, 11008, 2048), (32, 2048, 2048), (25, 1000, 1040),
     (30, 130, 4160), (19, 4864, 896),
+    # folded wide matrices (>= 256 row tiles, up to 3 tokens, short K)
+    (2, 5000, 2048), (3, 4096, 1040), (1, 8192, 1024),
 ]
 
 
