@@ -545,7 +545,13 @@ __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint
     xload(min(kt + XLEAD * KG, last), xset[i % XLEAD]);
     wload(min(kt + WLEAD * KG, last), wset[(i + WLEAD) % WSETS]);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+    // the MFMA phase at raised wave priority, so that when two workgroups
+    // share a SIMD the one in its MFMA phase issues first (the SwiGLU pair at
+    // 512 and 2048 tokens: 52.3 -> 50.5 us, 182 -> 175.5 us; single
+    // matrices unchanged)
+    __builtin_amdgcn_s_setprio(1);
     if (KG == 1 || kt < kt1) compute(wset[i % WSETS], i % 2);
+    __builtin_amdgcn_s_setprio(0);
     if (j + 1 < iters) xstore((i + 1) % 2, xset[(i + 1) % XLEAD]);
     __syncthreads();
   };
