@@ -71,8 +71,20 @@ def _require_gpu() -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
+# torch's current stream as a raw hipStream_t, without building a Stream
+# object per call (the public route costs a few microseconds of host time)
+_get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _raw_stream(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _get_raw_stream is not None:
+        return _get_raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
+
+
 def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return ctypes.c_void_p(_raw_stream(device))
 
 
 class _on_device:
@@ -335,7 +347,7 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
     q, s = weight._kernel_operands()
     lib = _native.load()
     with _on_device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _raw_stream(dev)
         ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, False)
         rc = lib.pgs_w8a16_linear_residual(_ptr(x2), _ptr(q), _ptr(s), _ptr(bb), _ptr(res), _ptr(y),
                                            _DTYPE_CODE[out_dtype], m, n, k, ws, ws_bytes, ctypes.c_void_p(stream))
@@ -361,7 +373,7 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     h = torch.empty_like(x2)
     lib = _native.load()
     with _on_device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
+        stream = _raw_stream(x.device)
         rc = lib.pgs_rmsnorm(_ptr(x2), _ptr(w), ctypes.c_float(eps), _ptr(h), x2.shape[0], k, ctypes.c_void_p(stream))
     check(rc, "rmsnorm")
     return h.reshape(x.shape)
@@ -413,7 +425,7 @@ def rope_qk(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: tor
     ko = (kc if inplace else torch.empty_like(kc)) if kc is not None else None
     lib = _native.load()
     with _on_device(qc.device):
-        stream = torch.cuda.current_stream(qc.device).cuda_stream
+        stream = _raw_stream(qc.device)
         rc = lib.pgs_rope(_ptr(qc), _ptr(qo), qh, _ptr(kc) if kc is not None else None,
                           _ptr(ko) if ko is not None else None, kh, _ptr(c), _ptr(s), m, hd,
                           ctypes.c_void_p(stream))
@@ -487,7 +499,7 @@ def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch
         outs[i].n = n
         ys.append(y)
     with _on_device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _raw_stream(dev)
         ws, ws_bytes = _workspace(lib, dev, stream, m, tuple(w.shape[0] for w in weights), k, False, nw is not None)
         if nw is None:
             rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
@@ -530,7 +542,7 @@ def _swiglu(x, gate, up, norm_weight, eps) -> torch.Tensor:
     nw = _norm_weight(norm_weight, k, dev, "rmsnorm_swiglu") if norm_weight is not None else None
     lib = _native.load()
     with _on_device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _raw_stream(dev)
         ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, True, nw is not None)
         if nw is None:
             rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, ws,
@@ -656,12 +668,21 @@ class QuantizedWeight:
         return obj
 
     def _kernel_operands(self) -> tuple[torch.Tensor, torch.Tensor]:
-        qp = self.qp
+        # cached for the current (qp, scale) objects when both are used as
+        # they are (no copy that an in-place update could leave stale);
+        # rebuilt when either is replaced (to(), assigning q)
+        qp0, sc0 = self.qp, self.scale
+        cached = getattr(self, "_ops", None)
+        if cached is not None and cached[0] is qp0 and cached[1] is sc0:
+            return cached[2], cached[3]
+        qp = qp0
         if not qp.is_contiguous() or (qp.numel() and qp.data_ptr() % 16):
             qp = _aligned(qp)
-        s = self.scale.reshape(-1)
+        s = sc0.reshape(-1)
         if s.dtype != torch.float32 or not s.is_contiguous():
             s = s.to(torch.float32).contiguous()
+        if qp is qp0 and (not s.numel() or s.data_ptr() == sc0.data_ptr()):
+            self._ops = (qp0, sc0, qp, s)
         return qp, s
 
 

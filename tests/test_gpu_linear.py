@@ -198,3 +198,19 @@ def test_bad_inputs_raise(gpu):
     odd = Q.QuantizedWeight(torch.randn(8, 40, device=gpu))
     with pytest.raises(ValueError, match="multiple of 16"):
         odd.linear(torch.zeros((2, 40), dtype=torch.bfloat16, device=gpu))
+
+
+def test_launch_stream_and_cached_operands(gpu):
+    """Launches go to torch's current stream (also a side stream), and the
+    cached kernel operands follow a weight whose storage is replaced."""
+    from pageserve_amd.quantization import _raw_stream
+    assert _raw_stream(gpu) == torch.cuda.current_stream(gpu).cuda_stream
+    side = torch.cuda.Stream(device=gpu)
+    with torch.cuda.stream(side):
+        assert _raw_stream(gpu) == side.cuda_stream
+    qw, q, s, x, _ = _problem(gpu, 5, 3, 256, 512)
+    xt = bf16_gpu(x, gpu)
+    report(to_np(qw.linear(xt)), O.linear(x, q, s), 512, "before")
+    q2 = np.ascontiguousarray(q[::-1])
+    qw.q = torch.from_numpy(q2).to(gpu)
+    report(to_np(qw.linear(xt)), O.linear(x, q2, s), 512, "after assigning q")
