@@ -28,7 +28,7 @@ def _problem(gpu, seed, m, n, k, bias=False):
     return qw, q, s, x, b
 
 
-# decode (skinny kernel, m <= 16) and prefill (tile kernel) shapes, including
+# decode (skinny kernel, m <= 32) and prefill (tile kernel) shapes, including
 # ragged n (not a multiple of 16 / 128) and k not a multiple of 64
 SHAPES = [
     (1, 2048, 2048), (1, 256, 2048), (1, 11008, 2048), (1, 2048, 11008),
