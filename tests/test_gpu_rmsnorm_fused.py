@@ -35,7 +35,7 @@ pytestmark = pytest.mark.gpu
 # (the 896 case has 14 chunks: unfolded, two staged slots past K), a
 # single wide matrix, and short groups that fold
 GROUPS = [([2048, 256, 256], 2048), ([896, 128, 128], 896), ([11008], 2048), ([2048], 11008), ([512, 64], 1024),
-          ([1104], 640)]
+          ([1104], 640), ([300, 48], 1040)]  # (K % 64 != 0: always the unfused route)
 
 
 def exact_sum_inputs(seed: int, m: int, k: int) -> np.ndarray:
@@ -53,7 +53,7 @@ def group(gpu, seed: int, ns: list[int], k: int):
     return ws, [Q.QuantizedWeight(torch.from_numpy(w).to(gpu)) for w in ws], [O.quantize_per_channel(w) for w in ws]
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16, 24])
 @pytest.mark.parametrize("ns,k", GROUPS)
 def test_rmsnorm_linear_group_equals_unfused(gpu, m, ns, k):
     _, qws, _ = group(gpu, 3 * k + len(ns), ns, k)
