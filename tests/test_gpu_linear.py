@@ -214,3 +214,35 @@ def test_launch_stream_and_cached_operands(gpu):
     q2 = np.ascontiguousarray(q[::-1])
     qw.q = torch.from_numpy(q2).to(gpu)
     report(to_np(qw.linear(xt)), O.linear(x, q2, s), 512, "after assigning q")
+
+
+def test_calls_from_a_worker_thread(gpu):
+    """The reference's runner calls forward_step from a daemon thread
+    (engine/runner.py:52-84): launches from another thread use that thread's
+    current stream, give the same results, and errors stay per thread."""
+    import threading
+
+    qw, q, s, x, _ = _problem(gpu, 61, 4, 2048, 2048)
+    xt = bf16_gpu(x, gpu)
+    main = qw.linear(xt)
+    out, errs = {}, []
+
+    def work():
+        try:
+            side = torch.cuda.Stream(device=gpu)
+            with torch.cuda.stream(side):
+                y = qw.linear(xt)
+                g = Q.swiglu(xt, qw, qw)
+            side.synchronize()
+            out["y"], out["g"] = y, g
+            with pytest.raises(ValueError):
+                qw.linear(xt[:, :100])
+        except BaseException as e:  # reported in the main thread
+            errs.append(e)
+
+    t = threading.Thread(target=work, daemon=True)
+    t.start()
+    t.join(60)
+    assert not t.is_alive() and not errs, errs
+    assert torch.equal(out["y"], main)
+    assert torch.equal(out["g"], Q.swiglu(xt, qw, qw))
