@@ -1,7 +1,7 @@
 """numpy restatement of pageserve's INT8 weight-only quantization arithmetic.
 
-TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the checker the HIP
-kernels are compared against, never part of the product.
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the reference results
+the HIP kernels are compared against, never part of the product.
 
 Reference: Rakshit-gen/pageserve ``engine/quantization.py`` and the call sites
 in ``engine/model.py``.  The reference runs these ops with PyTorch on the CPU;
