@@ -113,7 +113,7 @@ def dequantize(q: np.ndarray, scale: np.ndarray, dtype: str = "f32") -> np.ndarr
 
 
 # --------------------------------------------------------------------------
-# packed tile layout of the int8 weight (this build's storage format; no
+# packed tile layout of the int8 weight (pageserve_amd's storage format; no
 # counterpart in the reference, whose q is row-major)
 # --------------------------------------------------------------------------
 

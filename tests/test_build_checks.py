@@ -1,4 +1,4 @@
-"""The build's resource-usage check: the compiler's per-kernel remarks are
+"""The library compile's resource-usage check: the compiler's per-kernel remarks are
 parsed, and a kernel that spills registers to scratch fails the build."""
 
 from __future__ import annotations

@@ -354,7 +354,7 @@ def test_bf16_rounding_helper_is_round_to_nearest_even():
 
 
 # ---------------------------------------------------------------------------
-# the packed tile layout (this build's weight storage)
+# the packed tile layout (pageserve_amd's weight storage)
 # ---------------------------------------------------------------------------
 
 def test_packed_layout_lane_order():
