@@ -105,7 +105,7 @@ constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, b
 
 // FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
 // rows 8h .. 8h+7 of tile t.  XM > 0: up to XM tokens (M <= XM, NB > 0, K %
-// 64 == 0; folded, or NORM), their activations staged through LDS (below).
+// 64 == 0), their activations staged through LDS (below).
 // NORM: the activations are the rows of x after rms_norm with weight nw and
 // eps (engine/model.py:29-34), computed on the staged pieces (splits == 1:
 // the workgroup holds whole rows).  TM: 16-token column blocks (M <= 16 TM).
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
                                                          unsigned long long* __restrict__ pairs,
                                                          const uint16_t* __restrict__ nw, float eps) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
-  static_assert(XM == 0 || (NB > 0 && K64 && (FOLD || NORM)), "activation staging covers folded issue-once shapes");
+  static_assert(XM == 0 || (NB > 0 && K64 && 8 % XM == 0), "activation staging covers issue-once shapes");
   static_assert(!NORM || (XM > 0 && !OUT_F32), "the fused norm works on staged activations");
   static_assert(TM == 1 || (TM == 2 && !FOLD && XM == 0), "two token blocks: unfolded, direct activation loads");
   const int lane = threadIdx.x & 63;
@@ -495,14 +495,29 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   }
   // Up to four tokens in a folded launch stage their activations through
   // LDS (measured at one token: down_proj 6.56 -> 6.27 us, q|k|v 3.55 ->
-  // 3.38, o_proj 2.97 -> 3.03; at four tokens down_proj 7.24 -> 6.85; the
-  // unfolded SwiGLU pair, 4 chunks per wave, loses: 9.21 -> 9.33 us at one
-  // token, so it keeps direct loads).
+  // 3.38, o_proj 2.97 -> 3.03; at four tokens down_proj 7.24 -> 6.85).  An
+  // unfolded single matrix stages them at 3..8 tokens, where a lane's direct
+  // loads would repeat the last token in the idle columns (lm_head
+  // [151936, 2048] at 4 tokens 54.8 -> 48.1 us, at 8: 63.2 -> 56.1;
+  // 11008 x 2048 at 8: 7.6 -> 6.8; q|k|v at 8: 4.05 -> 3.82; down_proj's
+  // paired halves at 8: 8.2 -> 7.4); at 1..2 tokens the folded launch is
+  // faster, and the SwiGLU pair keeps direct loads (staged: 9.3 -> 9.5 us).
   if constexpr (NB > 0 && FOLD) {
     if (p.k % 64 == 0 && p.m <= 4) {
       if (p.m == 1) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, false>);
       if (p.m == 2) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, false>);
       return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, false>);
+    }
+  }
+  if constexpr (NB > 0 && !FOLD && NMAT == 1) {
+    if (p.k % 64 == 0 && p.m >= 3 && p.m <= 8) {
+      if (p.m <= 4) {
+        if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, 1, 4, false) <= kLdsLimit)
+          return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 4, false>);
+      } else {
+        if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, 1, 8, false) <= kLdsLimit)
+          return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 8, false>);
+      }
     }
   }
   if (p.k % 64 == 0) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0, false>);
@@ -571,10 +586,11 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   // tiles, which fill the CUs unsplit, only at up to 2 (q|k|v at one token:
   // 3.55 vs 3.62 us, at 4: 3.83 vs 3.82); o_proj: 3.0 vs 3.4 us at one token,
   // 3.4 vs 4.0 at 8.  With 256 tiles or more (lm_head, a lone gate_proj) a
-  // short K still folds at up to 3 tokens: the halves' two chunks per MFMA
+  // short K still folds at up to 2 tokens: the halves' two chunks per MFMA
   // and staged activations beat the unfolded launch (lm_head [151936, 2048]
-  // at one token 47.5 vs 52.0 us, at 3: 50.2 vs 53.2; 11008 x 2048 at one
-  // token 6.0 vs 6.6; even at 4, slower at 8).  Past the fold, a single matrix splits K over two
+  // at one token 47.1 vs 47.8 us staged unfolded, 52.0 unstaged; 11008 x
+  // 2048 5.9 vs 6.1); from 3 tokens the unfolded launch with staged
+  // activations is faster (lm_head at 3: 46.8 vs 50.2).  Past the fold, a single matrix splits K over two
   // workgroups when K is long or when at most 128 tiles meet several tokens
   // (o_proj at 16 tokens: 4.3 vs 4.8 us); otherwise a 32-chunk K is faster
   // unsplit, without the pair slot's round trip (q|k|v at 16 tokens: 4.7 vs
@@ -587,7 +603,7 @@ SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
   const int chunks = (k + 63) / 64;
   if (nmat == 1 && chunks >= 16 && m <= 8 &&
       ((tiles < 256 && (m <= 2 || (tiles <= 128 && (m <= 4 || chunks < 64)))) ||
-       (tiles >= 256 && m <= 3 && chunks < 64))) {
+       (tiles >= 256 && m <= 2 && chunks < 64))) {
     p.fold = true;
   } else if (can_split && tiles < 256) {
     if (nmat == 1 && chunks >= 16 && tiles * p.tm <= 256 &&

@@ -53,8 +53,12 @@ SHAPES = [
     # unsplit, K tails, a long K over few tiles
     (17, 2048, 2048), (24, 2048, 11008), (32, 11008, 2048), (32, 2048, 2048), (25, 1000, 1040),
     (30, 130, 4160), (19, 4864, 896),
-    # folded wide matrices (>= 256 row tiles, up to 3 tokens, short K)
-    (2, 5000, 2048), (3, 4096, 1040), (1, 8192, 1024),
+    # folded wide matrices (>= 256 row tiles, up to 2 tokens, short K)
+    (2, 5000, 2048), (1, 8192, 1024),
+    # unfolded single matrices at 3..8 tokens, activations staged (4 / 8 tokens):
+    # wide, 129..255 tiles, paired K halves, a long K over few tiles, 16-wave shapes
+    (3, 4096, 1024), (5, 4096, 2048), (8, 2560, 1024), (6, 2048, 11008), (7, 300, 8192),
+    (4, 5000, 4096), (8, 9000, 3072),
 ]
 
 
@@ -152,7 +156,8 @@ def test_paired_split_leaves_the_workspace_clean(gpu):
 
 
 @pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48),
-                                   (20, 2048, 2048), (32, 256, 2048), (27, 300, 1040)])
+                                   (20, 2048, 2048), (32, 256, 2048), (27, 300, 1040), (7, 4864, 896),
+                                   (6, 2048, 11008), (4, 4096, 1024)])
 def test_nonfinite_token_stays_in_its_row(gpu, m, n, k):
     """A token whose activations hold inf and nan poisons only its own
     outputs (as in x @ W^T): padding columns and the K range of another
