@@ -665,13 +665,17 @@ int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 // K % 64 == 0: the buffer-load kernel with two-step weight and activation
 // leads; the SwiGLU pair at 2 waves per SIMD, single matrices at 4, or, with
 // at most two work units per CU (o / q|k|v / down_proj at 512 tokens), in two
-// K groups per workgroup.  Other K: the pointer kernel (SwiGLU: one-step
+// K groups per workgroup, and a long K over at most one work unit per CU
+// (down_proj at 1024 tokens) in four.  Other K: the pointer kernel (SwiGLU: one-step
 // pipeline at the compiler's register budget; single matrices: two-step
 // pipeline at 4 waves per SIMD).
 template <int BM, int NMAT, bool OUT_F32>
 int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   if (ga.K % kBK == 0) {
     if constexpr (NMAT == 2) return launch_k64<BM, kBN, 2, OUT_F32, 2, 2, 2>(x, ga, st);
+    // a long K over at most one workgroup per CU: four K groups
+    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 256 && ga.K / kBK > 64)
+      return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
     if (static_cast<int64_t>(ga.tiles) * ga.splits <= 512) return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
     return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 4>(x, ga, st);
   }
@@ -735,9 +739,12 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   p.tiles_n = tiles_n;
   p.tiles = p.tiles_m * p.tiles_n;
   p.splits = 1;
-  // few output tiles: split K until about four workgroups per CU, keeping
-  // >= 32 K steps per split (>= 8 when there are very few tiles)
-  if (can_split) {
+  // fewer than 256 output tiles: split K until about four workgroups per CU,
+  // keeping >= 32 K steps per split (>= 8 when there are very few tiles).
+  // From 256 tiles on, K groups inside the workgroup beat a split and its
+  // reduce launch (down_proj at 1024 tokens 54 vs 58.5-64 us, at 2048: 99
+  // vs 105-110).
+  if (can_split && p.tiles < 256) {
     const int min_steps = p.tiles < 128 ? 8 : 32;
     while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 1024 && kb / (p.splits * 2) >= min_steps)
       p.splits *= 2;
