@@ -701,6 +701,10 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
                            : launch_k64<64, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
     }
   }
+  if constexpr (NMAT == 1) {
+    if (plan.bm == 128 && plan.bn == kBN && ga.K % kBK == 0) return launch_k64<128, kBN, 1, OUT_F32, 2, 2, 2>(x, ga, st);
+  }
+  if (plan.bm == 128) return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 gemm: no 128-token tile kernel for this shape");
   return plan.bm == 32 ? launch_bm<32, NMAT, OUT_F32>(x, ga, st) : launch_bm<64, NMAT, OUT_F32>(x, ga, st);
 }
 
@@ -732,6 +736,11 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
     return p;
   }
   p.bm = p.bn == 64 ? 128 : m <= 32 ? 32 : 64;
+  // a single matrix with very many 128-token tiles (lm_head at 256 tokens):
+  // 128 x 128 tiles read each weight panel half as often (lm_head [151936,
+  // 2048] at 256 tokens 165-176 vs 173-184 us; at 320..1376 tiles they are
+  // no faster or slower: q|k|v at 2048 tokens 32.5 vs 29.3 us)
+  if (nmat == 1 && k % kBK == 0 && p.bn == kBN && m >= 256 && tiles_for(128) >= 2048) p.bm = 128;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K
   if (nmat == 1 && p.bm == 64 && kb <= 64 && tiles_for(64) < 256) p.bm = 32;

@@ -137,6 +137,21 @@ def test_full_size_prefill_sampled(gpu):
     assert np.isfinite(y).all()
 
 
+def test_wide_matrix_128_token_tiles_sampled(gpu):
+    """A single matrix with very many 128-token tiles (as lm_head at 256
+    tokens) runs 128 x 128 tiles: ragged last token and row tiles, bias, bf16
+    output; a random sample of rows and columns against the oracle."""
+    m, n, k = 300, 87500, 512
+    qw, q, s, x, b = _problem(gpu, 5151, m, n, k, bias=True)
+    y = to_np(qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu)))
+    rng = np.random.default_rng(2)
+    rows = np.concatenate([rng.choice(m, 60, replace=False), [0, 255, 256, m - 1]])
+    cols = np.concatenate([rng.choice(n, 400, replace=False), [0, 127, 128, n - 1]])
+    ref = O.linear(x[rows], q[cols], s[cols], b[cols])
+    report(y[np.ix_(rows, cols)], ref, k, "128-token tiles sample")
+    assert np.isfinite(y).all()
+
+
 def test_paired_split_leaves_the_workspace_clean(gpu):
     """Decode shapes with few row tiles at 9..16 tokens split K in two and
     combine the halves through slots at the front of the shared workspace;
