@@ -210,6 +210,12 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     return round_to_bf16(t1 + t2)
 
 
+def linear_residual_intermediate(x, q, scale, bias=None) -> np.ndarray:
+    """The intermediate of :func:`linear_residual` with a bf16 output: the
+    linear output rounded to bf16 before the add."""
+    return round_to_bf16(linear(x, q, scale, bias))
+
+
 def linear_residual(x, q, scale, residual, bias=None, bf16_out: bool = True) -> np.ndarray:
     """``residual + F.linear(h, W, b)`` (engine/model.py:184, 190): the linear
     output is rounded to the output dtype first, then added to the bf16
@@ -239,14 +245,22 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
     return 2.0 ** (e - 7)
 
 
-def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False) -> dict:
+def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False,
+            ulp_of: np.ndarray | None = None) -> dict:
     """Error report of y against the oracle; ``ok`` when both bounds hold.
 
     ``rel`` = max|y - y_ref| / max|y_ref| must be <= 1e-2 and every element
     must satisfy |y - y_ref| <= 2e-2 * sqrt(k/1024).  For a bf16 output
-    (``bf16_out``) the elementwise bound is floored at one bf16 ulp of the
-    reference value: below that spacing no bf16 result can resolve the bound
-    (a value in [8, 16) already has a half-ulp of 0.031 > 2e-2 * sqrt(2)).
+    (``bf16_out``) the elementwise bound is floored at one bf16 ulp at the
+    larger of |y| and |y_ref|: below that spacing no bf16 result can resolve
+    the bound (a value in [8, 16) already has a half-ulp of 0.031 > 2e-2 *
+    sqrt(2)), and two bf16 values on either side of a power of two (an fp32
+    sum that differs from the float64 one in its last bits, rounded the other
+    way) are one ulp of the upper binade apart.  ``ulp_of``: further
+    magnitudes for that floor, elementwise -- the intermediate bf16 value of a
+    result rounded twice (residual + bf16(linear), engine/model.py:184): a
+    one-ulp difference there survives the sum, also when the sum cancels to
+    a smaller binade.
     """
     y = np.asarray(y, dtype=np.float64)
     r = np.asarray(y_ref, dtype=np.float64)
@@ -259,7 +273,10 @@ def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False) ->
     max_abs = float(diff.max())
     denom = float(np.abs(r).max())
     rel = max_abs / denom if denom > 0 else max_abs
-    bound = np.maximum(tol, bf16_ulp(r)) if bf16_out else tol
+    mag = np.maximum(np.abs(r), np.abs(y))
+    if ulp_of is not None:
+        mag = np.maximum(mag, np.abs(np.asarray(ulp_of, dtype=np.float64)))
+    bound = np.maximum(tol, bf16_ulp(mag)) if bf16_out else tol
     worst = float((diff / bound).max())
     ok = bool(np.isfinite(y).all()) and rel <= REL_TOL and worst <= 1.0
     return {"max_abs": max_abs, "rel": rel, "abs_tol": tol, "worst_vs_bound": worst, "ok": ok}

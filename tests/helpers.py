@@ -32,8 +32,8 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy()
 
 
-def report(y: np.ndarray, y_ref: np.ndarray, k: int, what: str, bf16_out: bool = True) -> dict:
+def report(y: np.ndarray, y_ref: np.ndarray, k: int, what: str, bf16_out: bool = True, ulp_of=None) -> dict:
     """Asserts the specification's tolerance (oracle.compare) and returns the report."""
-    r = O.compare(y, y_ref, k, bf16_out=bf16_out)
+    r = O.compare(y, y_ref, k, bf16_out=bf16_out, ulp_of=ulp_of)
     assert r["ok"], f"{what}: {r}"
     return r

@@ -92,6 +92,24 @@ def test_compare_floors_bf16_outputs_at_one_ulp():
     assert not O.compare(y3, ref, 2048, bf16_out=True)["ok"]
 
 
+def test_compare_floor_across_a_power_of_two_and_for_a_rounded_intermediate():
+    # reference just below 1.0 (ulp 2^-8), result 1.0: one ulp of the upper
+    # binade apart, which a K = 128 bound (0.00707) cannot resolve
+    ref = np.array([1 - 2 ** -7, 0.25], dtype=np.float32)
+    y = np.array([1.0, 0.25], dtype=np.float32)
+    assert O.compare(y, ref, 128, bf16_out=True)["ok"]
+    assert not O.compare(np.array([1 + 2 ** -7, 0.25], np.float32), ref, 128, bf16_out=True)["ok"]
+    # residual + bf16(linear) cancelling to a small sum: a one-ulp step of the
+    # intermediate (3.0 -> ulp 2^-6) is allowed only when the intermediate is given
+    # (a second element of typical size keeps the relative bound, max|dy| / max|ref|, out of the way)
+    ref2 = np.array([0.1015625, 4.0], dtype=np.float32)
+    inter = np.array([3.0, 1.0])
+    step = np.array([2 ** -6, 0.0], dtype=np.float32)
+    assert not O.compare(ref2 + step, ref2, 128, bf16_out=True)["ok"]
+    assert O.compare(ref2 + step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
+    assert not O.compare(ref2 + 2 * step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
+
+
 @pytest.mark.parametrize("v,ulp", [(1.0, 2 ** -7), (10.0, 2 ** -4), (0.5, 2 ** -8), (-3.0, 2 ** -6)])
 def test_bf16_ulp(v, ulp):
     assert O.bf16_ulp(np.array([v]))[0] == ulp

@@ -64,7 +64,8 @@ def test_linear_residual_matches_oracle(gpu, m, n, k, with_bias):
     xt, rt = bf16_gpu(x, gpu), bf16_gpu(r, gpu)
     bt = bf16_gpu(b, gpu) if with_bias else None
     y = qw.linear(xt, bt, residual=rt)
-    report(to_np(y), O.linear_residual(x, q, s, r, b), k, f"residual linear m={m} n={n} k={k}")
+    report(to_np(y), O.linear_residual(x, q, s, r, b), k, f"residual linear m={m} n={n} k={k}",
+           ulp_of=O.linear_residual_intermediate(x, q, s, b))
     # same roundings as the unfused kernel followed by a bf16 add
     unfused = (qw.linear(xt, bt).float() + rt.float()).to(torch.bfloat16)
     assert torch.equal(y, unfused)
@@ -81,7 +82,8 @@ def test_linear_residual_in_place_and_fp32(gpu):
     buf = bf16_gpu(r, gpu)
     out = qw.linear(xt, residual=buf, out=buf)  # x = residual + linear, in place
     assert out.data_ptr() == buf.data_ptr()
-    report(to_np(buf), O.linear_residual(x, q, s, r), k, "in-place residual")
+    report(to_np(buf), O.linear_residual(x, q, s, r), k, "in-place residual",
+           ulp_of=O.linear_residual_intermediate(x, q, s))
     y32 = qw.linear(xt, residual=bf16_gpu(r, gpu), out_dtype=torch.float32)
     report(to_np(y32), O.linear_residual(x, q, s, r, bf16_out=False), k, "fp32 residual", bf16_out=False)
 
@@ -113,7 +115,9 @@ def test_decode_layer_neighbours_chain(gpu):
     for j, nm in enumerate("qkv"):
         report(to_np(qkv[j]), O.linear(to_np(h), *qs[nm]), H, f"layer {nm}")
     report(to_np(h), h_ref, H, "layer rmsnorm 1")
-    report(to_np(x1), O.linear_residual(a, *qs["o"], x), H, "layer o + residual")
+    report(to_np(x1), O.linear_residual(a, *qs["o"], x), H, "layer o + residual",
+           ulp_of=O.linear_residual_intermediate(a, *qs["o"]))
     report(to_np(h2), O.rmsnorm(to_np(x1), ln2, 1e-6), H, "layer rmsnorm 2")
     act = O.swiglu(to_np(h2), *qs["g"], *qs["u"])
-    report(to_np(x2), O.linear_residual(O.round_to_bf16(act), *qs["d"], to_np(x1)), I, "layer down + residual")
+    report(to_np(x2), O.linear_residual(O.round_to_bf16(act), *qs["d"], to_np(x1)), I, "layer down + residual",
+           ulp_of=O.linear_residual_intermediate(O.round_to_bf16(act), *qs["d"]))

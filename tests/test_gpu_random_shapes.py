@@ -73,7 +73,7 @@ def test_random_shape(gpu, i):
     if kind == "residual":
         r = O.round_to_bf16(np.random.default_rng(26_000 + i).standard_normal((m, n)).astype(np.float32))
         y = qw.linear(xt, bt, residual=bf16_gpu(r, gpu))
-        report(to_np(y), O.linear_residual(x, q, s, r, b), k, what)
+        report(to_np(y), O.linear_residual(x, q, s, r, b), k, what, ulp_of=O.linear_residual_intermediate(x, q, s, b))
     else:
         y = qw.linear(xt, bt)
         report(to_np(y), O.linear(x, q, s, b), k, what)
