@@ -77,3 +77,50 @@ def test_random_shape(gpu, i):
     else:
         y = qw.linear(xt, bt)
         report(to_np(y), O.linear(x, q, s, b), k, what)
+
+
+# rms_norm fused into the projections (engine/model.py:166-170, 187-189):
+# random token counts around the fused / unfused boundary (4 tokens), K with
+# and without K % 64 == 0, groups and the SwiGLU pair
+NORM_CASES = int(os.environ.get("PGS_RANDOM_NORM_CASES", "24"))
+
+
+def _norm_case(i: int):
+    rng = np.random.default_rng(30_000 + i)
+    m = int(rng.integers(1, 9) if i % 2 == 0 else rng.integers(1, 40))
+    k = 64 * int(rng.integers(1, 80)) if i % 3 else 16 * int(rng.integers(1, 300))
+    n = int(rng.integers(1, 3000))
+    while m * n * k > MAX_WORK:
+        n = max(1, n // 2)
+    return m, n, k, ["group", "swiglu"][int(rng.integers(0, 2))], float(rng.choice([1e-6, 1e-5, 0.0]))
+
+
+@pytest.mark.parametrize("i", range(NORM_CASES))
+def test_random_fused_norm(gpu, i):
+    m, n, k, kind, eps = _norm_case(i)
+    what = f"norm case {i}: {kind} m={m} n={n} k={k} eps={eps}"
+    rng = np.random.default_rng(31_000 + i)
+    x = O.round_to_bf16(rng.standard_normal((m, k), dtype=np.float32) * np.float32(2.0))
+    w = O.round_to_bf16((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    # entries whose squares sum exactly in fp32 in any order: fused == unfused bit for bit
+    xe = rng.choice(np.array([0.5, -0.5, 1.0, -1.0, 2.0, -2.0], np.float32), size=(m, k))
+    xt, xet, wt = bf16_gpu(x, gpu), bf16_gpu(xe, gpu), bf16_gpu(w, gpu)
+    h = O.rmsnorm(x, w, eps)
+    if kind == "group":
+        ns = [n, max(1, n // 4)]
+        ws = [weights(32_000 + 10 * i + j, nn, k) for j, nn in enumerate(ns)]
+        qws = [Q.QuantizedWeight(torch.from_numpy(v).to(gpu)) for v in ws]
+        ys = Q.rmsnorm_linear_group(xt, wt, eps, qws)
+        for j, (v, y) in enumerate(zip(ws, ys)):
+            q, s = O.quantize_per_channel(v)
+            report(to_np(y), O.linear(h, q, s), k, f"{what} output {j}")
+        fused = Q.rmsnorm_linear_group(xet, wt, eps, qws)
+        plain = Q.linear_group(Q.rmsnorm(xet, wt, eps), qws)
+        assert all(torch.equal(a, b) for a, b in zip(fused, plain)), what
+    else:
+        wg, wu = weights(33_000 + i, n, k), weights(34_000 + i, n, k)
+        g, u = Q.QuantizedWeight(torch.from_numpy(wg).to(gpu)), Q.QuantizedWeight(torch.from_numpy(wu).to(gpu))
+        act = Q.rmsnorm_swiglu(xt, wt, eps, g, u)
+        ref = O.swiglu(h, *O.quantize_per_channel(wg), *O.quantize_per_channel(wu))
+        report(to_np(act), ref, k, what)
+        assert torch.equal(Q.rmsnorm_swiglu(xet, wt, eps, g, u), Q.swiglu(Q.rmsnorm(xet, wt, eps), g, u)), what
