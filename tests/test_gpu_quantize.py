@@ -186,3 +186,33 @@ def test_assigning_q_repacks(gpu):
     qw.q = new
     assert torch.equal(qw.q, new)
     np.testing.assert_array_equal(qw.qp.cpu().numpy(), O.pack_tiles(new.cpu().numpy()))
+
+
+# seeded random soak: any N and K, rows from denormal to 1e30 in magnitude,
+# zero rows and the adversarial tie rows, fp32 and bf16 inputs, row-major and
+# packed storage -- every q and scale bit-exact
+QUANT_CASES = int(__import__("os").environ.get("PGS_RANDOM_QUANT_CASES", "16"))
+
+
+@pytest.mark.parametrize("i", range(QUANT_CASES))
+def test_random_quantize_bit_exact(gpu, i):
+    rng = np.random.default_rng(40_000 + i)
+    n, k = int(rng.integers(1, 600)), int(rng.integers(1, 3000))
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    w = (w * (10.0 ** rng.uniform(-38, 30, size=(n, 1)))).astype(np.float32)
+    w[rng.random(n) < 0.05] = 0.0
+    if i % 3 == 0 and n >= 8 and k >= 8:
+        adv = adversarial_rows(rows=min(n, 32), per_row=min(k, 64))
+        w[: adv.shape[0], : adv.shape[1]] = adv
+    dtype = torch.bfloat16 if i % 2 else torch.float32
+    if dtype == torch.bfloat16:
+        w = O.round_to_bf16(w)
+        q_ref, s_ref = O.quantize_per_channel(O.f32_to_bf16_bits(w), bf16_bits=True)
+    else:
+        q_ref, s_ref = O.quantize_per_channel(w)
+    q, s = _gpu_quant(w, gpu, dtype)
+    _assert_bit_exact(q, s, q_ref, s_ref, f"case {i} [{n},{k}] {dtype}")
+    wt = torch.from_numpy(w).to(gpu) if dtype == torch.float32 else \
+        torch.from_numpy(O.f32_to_bf16_bits(w).view(np.int16).copy()).view(torch.bfloat16).to(gpu)
+    qw = Q.QuantizedWeight(wt)
+    _assert_bit_exact(qw.q.cpu().numpy(), qw.scale.cpu().numpy(), q_ref, s_ref, f"packed case {i} [{n},{k}] {dtype}")
