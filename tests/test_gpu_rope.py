@@ -81,3 +81,28 @@ def test_rope_errors(gpu):
         Q.rope_qk(q, None, c[:1], c[:1])
     with pytest.raises(ValueError):
         Q.rope_qk(q, torch.zeros(3, 2, 10, dtype=torch.bfloat16, device=gpu), c, c)
+
+
+# seeded random soak: token counts, head counts, head_dim (even, vector and
+# scalar paths), positions and theta
+ROPE_CASES = int(__import__("os").environ.get("PGS_RANDOM_ROPE_CASES", "16"))
+
+
+@pytest.mark.parametrize("i", range(ROPE_CASES))
+def test_random_rope_bit_exact(gpu, i):
+    rng = np.random.default_rng(50_000 + i)
+    m, qh = int(rng.integers(1, 300)), int(rng.integers(1, 33))
+    kh = int(rng.integers(0, qh + 1))
+    hd = 2 * int(rng.integers(1, 129))
+    start = int(rng.integers(0, 8192))
+    theta = float(rng.choice([1e4, 1e6]))
+    q = O.round_to_bf16(rng.standard_normal((m, qh, hd)).astype(np.float32) * np.float32(4.0))
+    k = O.round_to_bf16(rng.standard_normal((m, kh, hd)).astype(np.float32) * np.float32(4.0)) if kh else None
+    c, s = _cache(start + m, hd, theta)
+    c, s = c[start:start + m], s[start:start + m]
+    qo, ko = Q.rope_qk(bf16_gpu(q, gpu), bf16_gpu(k, gpu) if k is not None else None, c.to(gpu), s.to(gpu))
+    cf, sf = c.float().numpy(), s.float().numpy()
+    what = f"case {i}: m={m} qh={qh} kh={kh} hd={hd} start={start}"
+    assert np.array_equal(to_np(qo), O.rope(q, cf, sf)), what
+    if k is not None:
+        assert np.array_equal(to_np(ko), O.rope(k, cf, sf)), what
