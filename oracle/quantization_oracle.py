@@ -194,6 +194,30 @@ def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     return round_to_bf16((np.asarray(weight, dtype=np.float32) * t).astype(np.float32))
 
 
+def rmsnorm_bracket(x: np.ndarray, weight: np.ndarray, eps: float, ulps: int = 4) -> tuple[np.ndarray, np.ndarray]:
+    """Elementwise [lo, hi] of ``rms_norm`` over every r within ``ulps`` fp32
+    ulps of the correctly rounded r = rsqrt(mean(x^2) + eps).  An fp32 sum of
+    squares in another order moves r by a few ulps; where that flips the
+    inner rounding bf16(x * r), the multiply by the weight and the second
+    rounding carry the step into h (up to two bf16 ulps of h).  Every other
+    part of the formula is fixed, so a correct implementation lies inside the
+    bracket on every element.  h is monotone in r, so the extremes over the
+    2 ulps + 1 values of r bound it."""
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(weight, dtype=np.float32)
+    var = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float64))).astype(np.float32)
+    lo = hi = None
+    for k in range(-ulps, ulps + 1):
+        rk = r.copy()
+        for _ in range(abs(k)):
+            rk = np.nextafter(rk, np.float32(np.inf) if k > 0 else np.float32(0)).astype(np.float32)
+        h = round_to_bf16((w * round_to_bf16((x * rk).astype(np.float32))).astype(np.float32))
+        lo = h if lo is None else np.minimum(lo, h)
+        hi = h if hi is None else np.maximum(hi, h)
+    return lo, hi
+
+
 def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     """``apply_rope(x, cos, sin)`` (engine/model.py:53-56, ``rotate_half`` at
     :37-39) for bf16 tensors: ``x * cos + rotate_half(x) * sin`` where every

@@ -2,10 +2,10 @@
 and the residual add in the linear epilogue (engine/model.py:184, 190),
 against the oracle.
 
-RMSNorm: every element within one bf16 ulp of the oracle (the fp32 sum of
-squares is reduced in a different order than the oracle's correctly rounded
-mean, which can move r by an ulp), almost all equal, and repeat calls
-identical.  Residual linear: within the linear tolerance of the oracle's
+RMSNorm: every element inside the oracle's bracket (the formula evaluated
+at every r within 4 fp32 ulps of the correctly rounded r: the fp32 sum of
+squares is reduced in another order than the oracle's correctly rounded mean),
+almost all equal to the oracle, and repeat calls identical.  Residual linear: within the linear tolerance of the oracle's
 residual + bf16(linear); equal to the unfused kernel output plus a bf16 add
 (same roundings).
 """
@@ -33,9 +33,9 @@ def test_rmsnorm_matches_oracle(gpu, m, k):
     assert h.dtype == torch.bfloat16 and h.shape == (m, k)
     ref = O.rmsnorm(x, w, 1e-6)
     got = to_np(h)
-    diff = np.abs(got - ref)
-    assert np.all(diff <= O.bf16_ulp(ref)), f"max diff {diff.max()}"
-    assert np.mean(diff > 0) < 1e-3
+    lo, hi = O.rmsnorm_bracket(x, w, 1e-6)
+    assert np.all((lo <= got) & (got <= hi)), f"outside the bracket at {np.argwhere((got < lo) | (got > hi))[:5]}"
+    assert np.mean(got != ref) < 1e-3
     assert torch.equal(h, Q.rmsnorm(xt, wt, 1e-6))
 
 
@@ -121,3 +121,25 @@ def test_decode_layer_neighbours_chain(gpu):
     act = O.swiglu(to_np(h2), *qs["g"], *qs["u"])
     report(to_np(x2), O.linear_residual(O.round_to_bf16(act), *qs["d"], to_np(x1)), I, "layer down + residual",
            ulp_of=O.linear_residual_intermediate(O.round_to_bf16(act), *qs["d"]))
+
+
+# seeded random soak of the RMSNorm kernel: rows, widths (vector and scalar
+# paths), magnitudes and eps
+NORM_CASES = int(__import__("os").environ.get("PGS_RANDOM_RMSNORM_CASES", "16"))
+
+
+@pytest.mark.parametrize("i", range(NORM_CASES))
+def test_random_rmsnorm(gpu, i):
+    rng = np.random.default_rng(60_000 + i)
+    m, k = int(rng.integers(1, 400)), int(rng.integers(1, 9000))
+    scale = np.float32(10.0 ** rng.uniform(-3, 3))
+    x = O.round_to_bf16(rng.standard_normal((m, k), dtype=np.float32) * scale)
+    w = O.round_to_bf16((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    eps = float(rng.choice([1e-6, 1e-5, 0.0]))
+    got = to_np(Q.rmsnorm(bf16_gpu(x, gpu), bf16_gpu(w, gpu), eps))
+    ref = O.rmsnorm(x, w, eps)
+    lo, hi = O.rmsnorm_bracket(x, w, eps)
+    what = f"case {i}: m={m} k={k} scale={scale:.3g} eps={eps}"
+    out = np.argwhere((got < lo) | (got > hi))
+    assert out.size == 0, f"{what}: outside the bracket at {out[:5].tolist()}"
+    assert np.mean(got != ref) < 1e-2, what

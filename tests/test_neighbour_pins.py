@@ -91,3 +91,20 @@ def test_linear_residual_closed_forms():
     assert np.array_equal(O.linear_residual(np.zeros_like(x), q, s, r), r)
     # fp32 output: plain sum
     np.testing.assert_array_equal(O.linear_residual(x, q, s, r, bf16_out=False), O.linear(x, q, s) + r)
+
+
+def test_rmsnorm_bracket_holds_torch_and_the_oracle():
+    """The bracket of r within 4 fp32 ulps contains the oracle itself and
+    torch's CPU rms_norm (another reduction order) on every element, and is
+    tight: a planted mistake (no inner rounding) leaves it."""
+    for seed, (m, k) in enumerate([(64, 2048), (33, 896), (8, 11008), (100, 100)]):
+        x, w = _inputs(700 + seed, m, k)
+        lo, hi = O.rmsnorm_bracket(x, w, 1e-6)
+        for h in (O.rmsnorm(x, w, 1e-6), _torch_rms_norm(x, w, 1e-6)):
+            assert np.all((lo <= h) & (h <= hi))
+        assert np.mean(lo == hi) > 0.95
+        xf = np.asarray(x, np.float32)
+        var = np.mean(xf.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+        r = (1.0 / np.sqrt((var + np.float32(1e-6)).astype(np.float64))).astype(np.float32)
+        mutant = O.round_to_bf16((w * (xf * r)).astype(np.float32))  # no inner bf16 rounding
+        assert not np.all((lo <= mutant) & (mutant <= hi))
