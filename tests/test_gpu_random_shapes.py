@@ -110,12 +110,14 @@ def test_random_fused_norm(gpu, i):
         ns = [n, max(1, n // 4)]
         ws = [weights(32_000 + 10 * i + j, nn, k) for j, nn in enumerate(ns)]
         qws = [Q.QuantizedWeight(torch.from_numpy(v).to(gpu)) for v in ws]
-        ys = Q.rmsnorm_linear_group(xt, wt, eps, qws)
-        for j, (v, y) in enumerate(zip(ws, ys)):
+        bs = [O.round_to_bf16(rng.standard_normal(nn).astype(np.float32)) for nn in ns] if i % 4 < 2 else [None] * 2
+        bts = [bf16_gpu(b, gpu) if b is not None else None for b in bs]
+        ys = Q.rmsnorm_linear_group(xt, wt, eps, qws, bts)
+        for j, (v, b, y) in enumerate(zip(ws, bs, ys)):
             q, s = O.quantize_per_channel(v)
-            report(to_np(y), O.linear(h, q, s), k, f"{what} output {j}")
-        fused = Q.rmsnorm_linear_group(xet, wt, eps, qws)
-        plain = Q.linear_group(Q.rmsnorm(xet, wt, eps), qws)
+            report(to_np(y), O.linear(h, q, s, b), k, f"{what} output {j}")
+        fused = Q.rmsnorm_linear_group(xet, wt, eps, qws, bts)
+        plain = Q.linear_group(Q.rmsnorm(xet, wt, eps), qws, bts)
         assert all(torch.equal(a, b) for a, b in zip(fused, plain)), what
     else:
         wg, wu = weights(33_000 + i, n, k), weights(34_000 + i, n, k)
