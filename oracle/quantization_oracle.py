@@ -280,11 +280,12 @@ def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False,
     the bound (a value in [8, 16) already has a half-ulp of 0.031 > 2e-2 *
     sqrt(2)), and two bf16 values on either side of a power of two (an fp32
     sum that differs from the float64 one in its last bits, rounded the other
-    way) are one ulp of the upper binade apart.  ``ulp_of``: further
-    magnitudes for that floor, elementwise -- the intermediate bf16 value of a
-    result rounded twice (residual + bf16(linear), engine/model.py:184): a
-    one-ulp difference there survives the sum, also when the sum cancels to
-    a smaller binade.
+    way) are one ulp of the upper binade apart.  ``ulp_of``: the
+    intermediate bf16 value of a result rounded twice (residual +
+    bf16(linear), engine/model.py:184), elementwise: a one-ulp flip of the
+    intermediate survives the sum (also when the sum cancels to a smaller
+    binade) and the final rounding can add one ulp of the result, so the
+    floor becomes ulp(intermediate) + ulp(result).
     """
     y = np.asarray(y, dtype=np.float64)
     r = np.asarray(y_ref, dtype=np.float64)
@@ -297,10 +298,10 @@ def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False,
     max_abs = float(diff.max())
     denom = float(np.abs(r).max())
     rel = max_abs / denom if denom > 0 else max_abs
-    mag = np.maximum(np.abs(r), np.abs(y))
+    floor = bf16_ulp(np.maximum(np.abs(r), np.abs(y)))
     if ulp_of is not None:
-        mag = np.maximum(mag, np.abs(np.asarray(ulp_of, dtype=np.float64)))
-    bound = np.maximum(tol, bf16_ulp(mag)) if bf16_out else tol
+        floor = floor + bf16_ulp(np.asarray(ulp_of, dtype=np.float64))
+    bound = np.maximum(tol, floor) if bf16_out else tol
     worst = float((diff / bound).max())
     ok = bool(np.isfinite(y).all()) and rel <= REL_TOL and worst <= 1.0
     return {"max_abs": max_abs, "rel": rel, "abs_tol": tol, "worst_vs_bound": worst, "ok": ok}

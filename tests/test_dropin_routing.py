@@ -108,6 +108,13 @@ def test_compare_floor_across_a_power_of_two_and_for_a_rounded_intermediate():
     assert not O.compare(ref2 + step, ref2, 128, bf16_out=True)["ok"]
     assert O.compare(ref2 + step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
     assert not O.compare(ref2 + 2 * step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
+    # intermediate and result of similar size: the flip and the final rounding add up
+    ref3 = np.array([1.5, 4.0], dtype=np.float32)
+    inter3 = np.array([1.25, 1.0])
+    step3 = np.array([2 ** -6, 0.0], dtype=np.float32)   # = ulp(1.25) + ulp(1.5)
+    assert not O.compare(ref3 + step3, ref3, 48, bf16_out=True)["ok"]
+    assert O.compare(ref3 + step3, ref3, 48, bf16_out=True, ulp_of=inter3)["ok"]
+    assert not O.compare(ref3 + 2 * step3, ref3, 48, bf16_out=True, ulp_of=inter3)["ok"]
 
 
 @pytest.mark.parametrize("v,ulp", [(1.0, 2 ** -7), (10.0, 2 ** -4), (0.5, 2 ** -8), (-3.0, 2 ** -6)])

@@ -22,8 +22,10 @@ from pageserve_amd import quantization as Q
 
 pytestmark = pytest.mark.gpu
 
-# PGS_RANDOM_CASES raises the count for a longer soak of the launch plans
+# PGS_RANDOM_CASES raises the count for a longer soak of the launch plans;
+# PGS_RANDOM_START moves the window of seeded cases
 CASES = int(os.environ.get("PGS_RANDOM_CASES", "40"))
+START = int(os.environ.get("PGS_RANDOM_START", "0"))
 MAX_WORK = 1.2e8  # m * n * k of the oracle's float64 product
 
 
@@ -44,7 +46,7 @@ def _case(i: int):
     return m, n, k, kind, bool(rng.integers(0, 2))
 
 
-@pytest.mark.parametrize("i", range(CASES))
+@pytest.mark.parametrize("i", range(START, START + CASES))
 def test_random_shape(gpu, i):
     m, n, k, kind, bias = _case(i)
     what = f"case {i}: {kind} m={m} n={n} k={k} bias={bias}"
