@@ -16,6 +16,13 @@ Reported (one JSON line on stdout):
   prefill        the same sweep at M=512 in TFLOP/s vs the 2.5 PFLOP/s bf16
                  dense MFMA peak, with its own dominant-kernel roofline
   per_call_sweep the reference's call structure (7 separate linears/layer)
+  decode_detail  eager (no graph) time, the down_proj roofline, and one layer
+                 with its neighbours: RMSNorm inside the projections, as
+                 separate kernels, and as the reference's torch op chains
+  other_configs  decode at M=4 and 16, prefill at M=128 and 2048, the fused
+                 SwiGLU MLP, the int8 lm_head at M=1/8/256 (fp32 logits) and
+                 the single 4864x896 linear beside its CPU reference path
+  torch_gpu      the reference's computation with torch on this GPU
   cpu_baseline   the reference's per-call path (dequantize to bf16, then
                  F.linear) with torch on this host's CPU cores, on a sample
 """
