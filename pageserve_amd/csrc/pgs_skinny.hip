@@ -103,12 +103,23 @@ constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, b
   return (xm > 0 ? nw * nb * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
 }
 
-// FOLD: two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h owns
-// rows 8h .. 8h+7 of tile t.  XM > 0: up to XM tokens (M <= XM, NB > 0, K %
-// 64 == 0), their activations staged through LDS (below).
-// NORM: the activations are the rows of x after rms_norm with weight nw and
-// eps (engine/model.py:29-34), computed on the staged pieces (splits == 1:
-// the workgroup holds whole rows).  TM: 16-token column blocks (M <= 16 TM).
+// Template parameters:
+//   NW, U, NB  waves per workgroup, 64-k slots per batch, batches per wave
+//              issued at once (NB = 0: a loop over pairs of batches)
+//   NMAT       1 single matrix (q|k|v group members, o, down, lm_head);
+//              2 the SwiGLU pair (gate and up rows of the same index)
+//   OUT_F32    fp32 output (lm_head logits) instead of bf16
+//   K64        K % 64 == 0 (no masked K tail)
+//   FOLD       two workgroups per tile (splits == 1, M <= 8), workgroup 2t + h
+//              owns rows 8h .. 8h+7 of tile t
+//   XM         > 0: up to XM tokens (M <= XM, NB > 0, K % 64 == 0), their
+//              activations staged through LDS (below)
+//   NORM       the activations are the rows of x after rms_norm with weight nw
+//              and eps (engine/model.py:29-34), computed on the staged pieces
+//              (splits == 1: the workgroup holds whole rows)
+//   TM         16-token column blocks (M <= 16 TM; 2: unfolded, direct loads)
+// The launcher picks one combination per call (launch_kernel); the static
+// asserts below list the combinations that exist.
 template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM, bool NORM, int TM = 1>
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
