@@ -15,6 +15,10 @@
  * needed can serve all calls.  Calls that share a workspace must be ordered
  * (same stream, or synchronised); overlapping calls on one workspace race.
  * Passing NULL disables the split (always correct, slower for short-N shapes).
+ * Under HIP graph capture a graph replays with the workspace it was captured
+ * with: give each captured graph a workspace that it alone uses and zero it
+ * inside the capture (a kernel fill, recorded in the graph), so that every
+ * replay starts from empty slots whatever else used that memory meanwhile.
  *
  * Return value: PGS_OK (0) or one of the PGS_ERR_* codes below.  A call that
  * returns an error has launched nothing.  pgs_last_error() gives a
@@ -62,7 +66,7 @@ extern "C" {
 #define PGS_ERR_INVALID_ARGUMENT 1 /* bad size, null pointer, bad dtype code */
 #define PGS_ERR_MISALIGNED 2       /* pointer not aligned to its element size */
 #define PGS_ERR_LAUNCH 3           /* the HIP runtime rejected a kernel launch */
-#define PGS_ERR_NO_DEVICE 4        /* no usable gfx950 device */
+#define PGS_ERR_NO_DEVICE 4        /* no HIP device, or the stream's device is not a gfx950 */
 
 /* ABI version: bumped whenever a signature below changes. */
 int pgs_abi_version(void);
@@ -74,13 +78,34 @@ const char* pgs_error_string(int code);
 const char* pgs_last_error(void);
 
 /*
+ * Diagnostic, no counterpart in the reference: the kernel instance (with its
+ * template arguments), grid size and K split of the calling thread's most
+ * recent launch by a linear entry point ("" if none).  Lets tests and
+ * profiles name the launch plan a shape takes.
+ */
+const char* pgs_last_plan(void);
+
+/*
+ * Whether `stream` is being captured into a HIP graph: *capturing = 1 and
+ * *capture_id = the capture's id while a capture is active (2 if it was
+ * invalidated), else 0 and 0.  No counterpart in the reference; hosts use it
+ * to give each captured graph its own workspace (see the workspace notes
+ * above).
+ */
+int pgs_stream_capture_state(void* stream, int* capturing, unsigned long long* capture_id);
+
+/*
  * Replaces quantize_per_channel(weight) -- engine/quantization.py:16-23.
  *   absmax[r] = max(max_j |w[r,j]|, 1e-8f)
  *   scale[r]  = absmax[r] / 127.0f                 (IEEE fp32 division)
  *   q[r,j]    = clamp(rint(w[r,j] / scale[r]), -127, 127)   (ties to even)
  * Bit-exact with the reference's CPU arithmetic.  w_dtype: PGS_DTYPE_F32 or
  * PGS_DTYPE_BF16 (a bf16 weight widens exactly, as weight.float() does).
- * Non-finite weights give unspecified q/scale, as in the reference.
+ * Non-finite weights follow the reference's CPU arithmetic: a row holding a
+ * NaN gets a NaN scale (torch's amax and clamp keep NaN), a row holding an
+ * infinity and no NaN gets an infinite scale, and every quotient that is NaN
+ * (NaN / s, inf / inf, w / NaN) becomes q = 0, the value torch's CPU
+ * conversion of NaN to int8 gives; finite / inf is 0.
  */
 int pgs_quantize_per_channel(const void* w, int w_dtype, int64_t n, int64_t k,
                              int8_t* q, float* scale, void* stream);

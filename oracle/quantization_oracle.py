@@ -89,7 +89,7 @@ def quantize_per_channel(weight: np.ndarray, *, bf16_bits: bool = False):
     with np.errstate(divide="ignore", invalid="ignore"):
         ratio = (w / scale).astype(np.float32)
     q = np.clip(np.rint(ratio), F32(-127.0), F32(127.0))
-    q = np.nan_to_num(q, nan=0.0).astype(np.int8)  # NaN: unspecified in the reference
+    q = np.nan_to_num(q, nan=0.0).astype(np.int8)  # NaN -> 0: torch's CPU int8 conversion of NaN
     return q, scale
 
 
@@ -269,23 +269,87 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
     return 2.0 ** (e - 7)
 
 
+U32 = 2.0 ** -24  # unit roundoff of fp32
+
+
+def acc_bound(x: np.ndarray, q: np.ndarray, scale: np.ndarray, bias: np.ndarray | None = None,
+              dx: np.ndarray | None = None) -> np.ndarray:
+    """Elementwise bound on how far an fp32 evaluation of :func:`linear` can
+    be from the exact value, whatever the summation order: the products
+    x_i * q_i are exact in fp32 (8 + 8 significant bits), at most K additions
+    and the scale multiply and bias add each round once, so the error is at
+    most (K + 8) * u * (s * sum_i |x_i q_i| + |b|) with u = 2^-24 (first order;
+    the margin of 8 covers the cross-wave and split sums and the second-order
+    terms).  ``dx``: an elementwise bound on how far the kernel's input may
+    be from ``x`` (an RMSNorm computed in another summation order), which
+    moves the output by at most |dx| |W|^T.  float64, shape [M, N]."""
+    k = np.asarray(q).shape[1]
+    w = np.abs(dequantize(q, scale, "f32").astype(np.float64))
+    s = np.abs(np.asarray(x, dtype=np.float64)) @ w.T
+    if bias is not None:
+        s = s + np.abs(np.asarray(bias, dtype=np.float64)).reshape(1, -1)
+    out = (k + 8) * U32 * s
+    if dx is not None:
+        out = out + np.abs(np.asarray(dx, dtype=np.float64)) @ w.T
+    return out
+
+
+def swiglu_acc(x, q_gate, s_gate, q_up, s_up, dx=None) -> np.ndarray:
+    """Elementwise bound on how far an fp32 evaluation of :func:`swiglu` can
+    be from the exact value: the gate and up sums carry :func:`acc_bound`
+    errors dg, du; act = silu(g) * u moves by at most |silu'| dg |u| +
+    |silu(g)| du + dg du (|silu'| <= 1.1 everywhere; its value at g is used),
+    and the fp32 evaluation of silu (exp, add, divide) and the product add
+    at most 16 u |act|.  ``dx`` as for :func:`acc_bound`."""
+    g = linear(x, q_gate, s_gate).astype(np.float64)
+    u = linear(x, q_up, s_up).astype(np.float64)
+    dg = acc_bound(x, q_gate, s_gate, dx=dx)
+    du = acc_bound(x, q_up, s_up, dx=dx)
+    sig = 1.0 / (1.0 + np.exp(-g))
+    dsilu = np.abs(sig * (1.0 + g * (1.0 - sig))) + dg  # the slope anywhere within dg of g (|silu''| <= 0.5)
+    return dsilu * dg * np.abs(u) + np.abs(g * sig) * du + dg * du + 16 * U32 * np.abs(g * sig * u)
+
+
+def mlp_acc(x, q_gate, s_gate, q_up, s_up, q_down, s_down) -> np.ndarray:
+    """Elementwise bound for :func:`mlp` evaluated as the kernels do it: the
+    SwiGLU activations rounded once to bf16 (half an ulp plus
+    :func:`swiglu_acc` from the exact ones) feed the down projection, whose
+    own accumulation adds :func:`acc_bound`."""
+    act = swiglu(x, q_gate, s_gate, q_up, s_up)
+    dact = 0.5 * bf16_ulp(act) + swiglu_acc(x, q_gate, s_gate, q_up, s_up)
+    return acc_bound(act, q_down, s_down, dx=dact)
+
+
+def rmsnorm_dx(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """Elementwise width of :func:`rmsnorm_bracket`: how far an RMSNorm in
+    another fp32 summation order may be from :func:`rmsnorm`."""
+    lo, hi = rmsnorm_bracket(x, weight, eps)
+    return np.abs(hi.astype(np.float64) - lo.astype(np.float64))
+
+
 def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False,
-            ulp_of: np.ndarray | None = None) -> dict:
+            ulp_of: np.ndarray | None = None, acc=None) -> dict:
     """Error report of y against the oracle; ``ok`` when both bounds hold.
 
     ``rel`` = max|y - y_ref| / max|y_ref| must be <= 1e-2 and every element
-    must satisfy |y - y_ref| <= 2e-2 * sqrt(k/1024).  For a bf16 output
-    (``bf16_out``) the elementwise bound is floored at one bf16 ulp at the
-    larger of |y| and |y_ref|: below that spacing no bf16 result can resolve
-    the bound (a value in [8, 16) already has a half-ulp of 0.031 > 2e-2 *
-    sqrt(2)), and two bf16 values on either side of a power of two (an fp32
-    sum that differs from the float64 one in its last bits, rounded the other
-    way) are one ulp of the upper binade apart.  ``ulp_of``: the
-    intermediate bf16 value of a result rounded twice (residual +
-    bf16(linear), engine/model.py:184), elementwise: a one-ulp flip of the
-    intermediate survives the sum (also when the sum cancels to a smaller
-    binade) and the final rounding can add one ulp of the result, so the
-    floor becomes ulp(intermediate) + ulp(result).
+    must satisfy |y - y_ref| <= 2e-2 * sqrt(k/1024).
+
+    bf16 outputs (``bf16_out``): a correctly rounded bf16 result of an fp32
+    value that is within ``acc`` of the exact one lies within half a bf16 ulp
+    + ``acc`` of the oracle's (unrounded) value, so the elementwise bound is
+    floored there: half an ulp at the larger of |y| and |y_ref| (two results
+    on either side of a power of two are half an ulp of the upper binade from
+    the value between them) plus ``acc``, the elementwise accumulation bound
+    (:func:`acc_bound`, :func:`swiglu_acc`), which a single-rounding bf16
+    comparison must be given.  Below that spacing no bf16 result can resolve
+    the stated bound (a value in [8, 16) has a half-ulp of 0.031 > 2e-2 *
+    sqrt(2)).  ``ulp_of``: the intermediate bf16 value of a result rounded
+    twice (residual + bf16(linear), engine/model.py:184) against an oracle
+    that rounds the same twice: the two intermediates may sit on either side
+    of a rounding midpoint, one ulp apart, and that step survives the sum
+    (also when it cancels to a smaller binade) while the final rounding can
+    add one ulp of the result, so the floor is ulp(intermediate) +
+    ulp(result) (+ ``acc`` when given).
     """
     y = np.asarray(y, dtype=np.float64)
     r = np.asarray(y_ref, dtype=np.float64)
@@ -294,13 +358,18 @@ def compare(y: np.ndarray, y_ref: np.ndarray, k: int, bf16_out: bool = False,
     tol = abs_tol(k)
     if y.size == 0:
         return {"max_abs": 0.0, "rel": 0.0, "abs_tol": tol, "ok": True}
+    if bf16_out and ulp_of is None and acc is None:
+        raise ValueError("compare: a single-rounding bf16 comparison needs the accumulation bound `acc`")
     diff = np.abs(y - r)
     max_abs = float(diff.max())
     denom = float(np.abs(r).max())
     rel = max_abs / denom if denom > 0 else max_abs
-    floor = bf16_ulp(np.maximum(np.abs(r), np.abs(y)))
+    big = np.maximum(np.abs(r), np.abs(y))
+    extra = np.zeros_like(diff) if acc is None else np.broadcast_to(np.asarray(acc, dtype=np.float64), diff.shape)
     if ulp_of is not None:
-        floor = floor + bf16_ulp(np.asarray(ulp_of, dtype=np.float64))
+        floor = bf16_ulp(big) + bf16_ulp(np.asarray(ulp_of, dtype=np.float64)) + extra
+    else:
+        floor = 0.5 * bf16_ulp(big) + extra
     bound = np.maximum(tol, floor) if bf16_out else tol
     worst = float((diff / bound).max())
     ok = bool(np.isfinite(y).all()) and rel <= REL_TOL and worst <= 1.0

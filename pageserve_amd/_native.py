@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class NativeLibraryError(RuntimeError):
@@ -52,6 +52,8 @@ SIGNATURES = {
     "pgs_abi_version": (_INT, []),
     "pgs_error_string": (ctypes.c_char_p, [_INT]),
     "pgs_last_error": (ctypes.c_char_p, []),
+    "pgs_last_plan": (ctypes.c_char_p, []),
+    "pgs_stream_capture_state": (_INT, [_VP, ctypes.POINTER(_INT), ctypes.POINTER(ctypes.c_ulonglong)]),
     "pgs_quantize_per_channel": (_INT, [_VP, _INT, _I64, _I64, _VP, _VP, _VP]),
     "pgs_dequantize": (_INT, [_VP, _VP, _I64, _I64, _VP, _INT, _VP]),
     "pgs_quantize_per_channel_packed": (_INT, [_VP, _INT, _I64, _I64, _VP, _VP, _VP]),
@@ -93,6 +95,13 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         if _lib is not None and path is None:
             return _lib
         p = Path(path) if path is not None else LIB_PATH
+        # torch first: its HIP runtime (soname libamdhip64.so.7) is then the
+        # one the library binds to, so streams and pointers from torch are
+        # valid handles for the library's launches
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not p.exists():
             raise NativeLibraryError(
                 f"pageserve_amd: gfx950 library not found at {p}; build it with "
@@ -112,6 +121,20 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+def last_plan() -> str:
+    """Kernel instance, grid and K split of this thread's last linear launch."""
+    return load().pgs_last_plan().decode(errors="replace")
+
+
+def capture_state(stream: int) -> tuple[int, int]:
+    """(capturing, capture id) of a raw hipStream_t (0, 0 when not capturing)."""
+    lib = load()
+    cap, cid = _INT(0), ctypes.c_ulonglong(0)
+    rc = lib.pgs_stream_capture_state(ctypes.c_void_p(stream), ctypes.byref(cap), ctypes.byref(cid))
+    check(rc, "stream capture state")
+    return cap.value, cid.value
 
 
 def check(rc: int, what: str) -> None:

@@ -102,6 +102,20 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int fill_zero(void* p, int64_t bytes, hipStream_t st);  // kernel fill (no memset node in captured graphs)
 
+// Devices the library tracks per device state for (architecture, scratch).
+constexpr int kMaxDevices = 64;
+// The device a stream launches on (the current device for the null stream).
+int stream_device(hipStream_t st, int* dev);
+// PGS_OK when the stream's device is a gfx950 (checked once per device),
+// else PGS_ERR_NO_DEVICE with a message.  Every launching entry point calls
+// it after its argument checks and before its first launch.
+int require_device(const char* fn, hipStream_t st);
+
+// Records the calling thread's last linear launch (pgs_last_plan): `kernel`
+// is a static string naming the kernel instance, `second` an optional
+// follow-up kernel (the split-K reduce).
+void note_launch(const char* kernel, long long grid, int splits, const char* second = nullptr);
+
 inline bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }

@@ -638,6 +638,7 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
 template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
 int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
+  note_launch(__PRETTY_FUNCTION__, grid, ga.splits, ga.splits > 1 ? "gemm_reduce_kernel" : nullptr);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, NMAT, OUT_F32, OCC, LEAD>), dim3(static_cast<unsigned>(grid)),
                      dim3(kThreads), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
@@ -651,6 +652,7 @@ int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG = 1>
 int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
+  note_launch(__PRETTY_FUNCTION__, grid, ga.splits, ga.splits > 1 ? "gemm_reduce_kernel" : nullptr);
   hipLaunchKernelGGL((gemm_k64_kernel<BM, BN, NMAT, OUT_F32, WLEAD, XLEAD, OCC, KG>), dim3(static_cast<unsigned>(grid)),
                      dim3(kThreads * KG), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");

@@ -72,6 +72,11 @@ size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat);
 bool skinny_norm_fusable(const SkinnyPlan& p, int m, int k, bool out_f32, int nmat);
 int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st);
 
+// pgs_w8a16_linear_group with the entry point's name `fn` in its messages
+// (for entry points that supply their own workspace).
+int linear_call(const char* fn, const void* x, const pgs_linear_out* outs, int n_outs, int y_dtype, int64_t m,
+                int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
 GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool can_split);
 size_t gemm_partial_bytes(const GemmPlan& p, int nmat);
 int launch_gemm(Problem& p, const GemmPlan& plan, hipStream_t st);

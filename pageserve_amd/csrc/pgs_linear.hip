@@ -55,6 +55,7 @@ size_t norm_offset(size_t linear_bytes) {
 }
 
 int run(Problem& p, void* workspace, size_t ws_bytes, hipStream_t st) {
+  if (int rc = require_device("w8a16 linear", st)) return rc;
   const int members = (p.nmat == 2) ? 1 : p.args.n_outs;
   const Plan plan = make_plan(p.m, p.k, p.nmat, p.args.n, members, workspace != nullptr);
   const size_t need = workspace_bytes(plan, p.nmat);
@@ -201,6 +202,13 @@ int linear_group_impl(const char* fn, const void* x, const pgs_linear_out* outs,
 }
 
 }  // namespace
+
+namespace pgs {
+int linear_call(const char* fn, const void* x, const pgs_linear_out* outs, int n_outs, int y_dtype, int64_t m,
+                int64_t k, void* workspace, size_t workspace_bytes_, void* stream) {
+  return linear_group_impl(fn, x, outs, nullptr, n_outs, y_dtype, m, k, workspace, workspace_bytes_, stream);
+}
+}  // namespace pgs
 
 extern "C" int pgs_w8a16_linear_group(const void* x, const pgs_linear_out* outs, int n_outs, int y_dtype,
                                       int64_t m, int64_t k, void* workspace, size_t workspace_bytes_,

@@ -90,6 +90,7 @@ extern "C" int pgs_rmsnorm(const void* x, const void* weight, float eps, void* h
   if (!aligned(x, 2) || !aligned(weight, 2) || !aligned(h, 2)) return fail(PGS_ERR_MISALIGNED, "pgs_rmsnorm: misaligned");
   if (!(eps >= 0.f)) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_rmsnorm: eps must be >= 0");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = require_device("pgs_rmsnorm", st)) return rc;
   const bool vec = k % 8 == 0 && aligned(x, 16) && aligned(weight, 16) && aligned(h, 16);
   const auto* xp = reinterpret_cast<const uint16_t*>(x);
   const auto* wp = reinterpret_cast<const uint16_t*>(weight);

@@ -128,6 +128,7 @@ extern "C" int pgs_pack_weight(const int8_t* q, int64_t n, int64_t k, int8_t* pa
   if (!aligned(packed, 16)) return fail(PGS_ERR_MISALIGNED, "pgs_pack_weight: packed buffer not 16-byte aligned");
   const int64_t kb = packed_kblocks(k), nseg = packed_bytes(n, k) / 16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if ((rc = require_device("pgs_pack_weight", st))) return rc;
   if (k % 16 == 0 && aligned(q, 16))
     hipLaunchKernelGGL(pack_kernel<true>, dim3(blocks_for(nseg)), dim3(256), 0, st, q, n, k, kb, nseg, packed);
   else
@@ -143,6 +144,7 @@ extern "C" int pgs_unpack_weight(const int8_t* packed, int64_t n, int64_t k, int
   if (!aligned(packed, 16)) return fail(PGS_ERR_MISALIGNED, "pgs_unpack_weight: packed buffer not 16-byte aligned");
   const int64_t kb = packed_kblocks(k), nseg = packed_bytes(n, k) / 16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if ((rc = require_device("pgs_unpack_weight", st))) return rc;
   if (k % 16 == 0 && aligned(q, 16))
     hipLaunchKernelGGL(unpack_kernel<true>, dim3(blocks_for(nseg)), dim3(256), 0, st, packed, n, k, kb, nseg, q);
   else
@@ -160,6 +162,9 @@ extern "C" int pgs_dequantize_packed(const int8_t* packed, const float* scale, i
     return fail(PGS_ERR_MISALIGNED, "pgs_dequantize_packed: packed/scale misaligned");
   const int64_t kb = packed_kblocks(k), nseg = packed_bytes(n, k) / 16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (out_dtype != PGS_DTYPE_F32 && out_dtype != PGS_DTYPE_BF16 && out_dtype != PGS_DTYPE_F16)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_dequantize_packed: output dtype code %d not supported", out_dtype);
+  if ((rc = require_device("pgs_dequantize_packed", st))) return rc;
   switch (out_dtype) {
     case PGS_DTYPE_F32:
       if (!aligned(out, 4)) return fail(PGS_ERR_MISALIGNED, "pgs_dequantize_packed: output misaligned");

@@ -45,9 +45,17 @@ __device__ __forceinline__ void load_row_vec(const void* __restrict__ base, int6
   }
 }
 
+// max that propagates NaN, as torch's amax does (fmaxf would drop it): a row
+// holding a NaN gets a NaN scale, as in the reference
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return a != a ? a : (b != b ? b : fmaxf(a, b));
+}
+
 __device__ __forceinline__ uint32_t quantize_one(float w, float s) {
   float r = rintf(w / s);  // IEEE divide, ties-to-even
-  if (!(r == r)) return 0u;  // NaN (non-finite input; unspecified upstream)
+  // NaN (a NaN or infinite weight, or a row with a NaN scale): 0, which is
+  // what the reference's int8 conversion of NaN gives on the CPU
+  if (!(r == r)) return 0u;
   r = fminf(fmaxf(r, -127.0f), 127.0f);
   return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(r))));
 }
@@ -67,17 +75,18 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
     float f[VEC];
     load_row_vec<BF16, VEC>(w, base + v * VEC, f);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    for (int i = 0; i < VEC; ++i) amax = nan_max(amax, fabsf(f[i]));
   }
 #pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  for (int off = kWave / 2; off > 0; off >>= 1) amax = nan_max(amax, __shfl_xor(amax, off));
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
   __syncthreads();
   amax = red[0];
 #pragma unroll
-  for (int i = 1; i < kQuantThreads / kWave; ++i) amax = fmaxf(amax, red[i]);
+  for (int i = 1; i < kQuantThreads / kWave; ++i) amax = nan_max(amax, red[i]);
 
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;  // :20 clamp(min=1e-8), :21 / 127.0
+  // :20 clamp(min=1e-8) (a NaN stays NaN, as torch's clamp keeps it), :21 / 127.0
+  const float s = (amax != amax ? amax : fmaxf(amax, 1e-8f)) / 127.0f;
   if (threadIdx.x == 0) scale[row] = s;
 
   for (int64_t v = threadIdx.x; v < nvec; v += kQuantThreads) {
@@ -189,6 +198,7 @@ int launch_quantize(const char* fn, const void* w, int w_dtype, int64_t n, int64
   if (!aligned(w, esz) || !aligned(scale, 4))
     return fail(PGS_ERR_MISALIGNED, "%s: weight/scale not aligned to element size", fn);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = require_device(fn, st)) return rc;
   const int64_t kb = packed_kblocks(k);
   if (PACKED && k > 0 && (n % 16 != 0 || k % 64 != 0)) {
     // padding rows/columns of the packed buffer must read as zero
@@ -235,6 +245,9 @@ extern "C" int pgs_dequantize(const int8_t* q, const float* scale, int64_t n, in
   if (n * k / 16 > 0x7fffffffLL * 256LL)
     return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_dequantize: tensor too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (out_dtype != PGS_DTYPE_F32 && out_dtype != PGS_DTYPE_BF16 && out_dtype != PGS_DTYPE_F16)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_dequantize: output dtype code %d not supported", out_dtype);
+  if (int rc = require_device("pgs_dequantize", st)) return rc;
   switch (out_dtype) {
     case PGS_DTYPE_F32:
       if (!aligned(out, 4)) return fail(PGS_ERR_MISALIGNED, "pgs_dequantize: fp32 output not 4-byte aligned");

@@ -106,6 +106,7 @@ extern "C" int pgs_rope(const void* q, void* q_out, int64_t q_heads, const void*
   const int64_t blocks = (units + kRopeThreads - 1) / kRopeThreads;
   if (blocks > 0x7fffffff) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_rope: too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = require_device("pgs_rope", st)) return rc;
   const auto* qp = reinterpret_cast<const uint16_t*>(q);
   const auto* kp = reinterpret_cast<const uint16_t*>(k);
   auto* qo = reinterpret_cast<uint16_t*>(q_out);

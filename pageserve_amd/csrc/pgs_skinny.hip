@@ -469,25 +469,30 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GroupArgs a, int M, 
   }
 }
 
-template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool FOLD>
-int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
+// Launches one skinny_kernel instance (and records it for pgs_last_plan:
+// this function's pretty name spells out the instance's template arguments).
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, int XM, bool NORM, int TM = 1>
+int launch_instance(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   const int64_t grid = static_cast<int64_t>(plan.tiles) * (FOLD ? 2 : plan.splits);
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
-  const dim3 g(static_cast<unsigned>(grid)), b(64 * NW);
-  auto go = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, g, b, 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs, p.norm_w, p.eps);
-    return check_launch("w8a16 skinny kernel");
-  };
+  note_launch(__PRETTY_FUNCTION__, grid, plan.splits, plan.splits > 1 && !plan.pair ? "skinny_reduce_kernel" : nullptr);
+  hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, K64, FOLD, XM, NORM, TM>), dim3(static_cast<unsigned>(grid)),
+                     dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs, p.norm_w, p.eps);
+  return check_launch("w8a16 skinny kernel");
+}
+
+template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool FOLD>
+int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   if constexpr (NB > 0 && !OUT_F32) {
     // rms_norm applied to the staged activations
     if (p.norm_w) {
       if (p.k % 64 != 0 || p.m > 4 || plan.splits != 1 || plan.pair)
         return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm needs m <= 4 and one K range");
       constexpr int S = FOLD ? 2 : 1;
-      if (p.m == 1) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, true>);
-      if (p.m == 2) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, true>);
+      if (p.m == 1) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, true>(p, plan, st);
+      if (p.m == 2) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, true>(p, plan, st);
       if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, S, 4, true) <= kLdsLimit)
-        return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, true>);
+        return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, true>(p, plan, st);
       return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: the fused norm's staging exceeds LDS");
     }
   }
@@ -498,8 +503,8 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
     if constexpr (!FOLD && NW >= 8 && (NB == 2 || NB == 0)) {
       if (p.m > 32 || plan.tm != 2)
         return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: m=%d with %d token blocks", p.m, plan.tm);
-      if (p.k % 64 == 0) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 0, false, 2>);
-      return go(skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, false, 0, false, 2>);
+      if (p.k % 64 == 0) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, false, 0, false, 2>(p, plan, st);
+      return launch_instance<NW, U, 0, NMAT, OUT_F32, false, false, 0, false, 2>(p, plan, st);
     } else {
       return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: no two-block kernel for this launch shape (m=%d)", p.m);
     }
@@ -515,24 +520,24 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   // faster, and the SwiGLU pair keeps direct loads (staged: 9.3 -> 9.5 us).
   if constexpr (NB > 0 && FOLD) {
     if (p.k % 64 == 0 && p.m <= 4) {
-      if (p.m == 1) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, false>);
-      if (p.m == 2) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, false>);
-      return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, false>);
+      if (p.m == 1) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, false>(p, plan, st);
+      if (p.m == 2) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, false>(p, plan, st);
+      return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, false>(p, plan, st);
     }
   }
   if constexpr (NB > 0 && !FOLD && NMAT == 1) {
     if (p.k % 64 == 0 && p.m >= 3 && p.m <= 8) {
       if (p.m <= 4) {
         if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, 1, 4, false) <= kLdsLimit)
-          return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 4, false>);
+          return launch_instance<NW, U, NB, NMAT, OUT_F32, true, false, 4, false>(p, plan, st);
       } else {
         if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, 1, 8, false) <= kLdsLimit)
-          return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, false, 8, false>);
+          return launch_instance<NW, U, NB, NMAT, OUT_F32, true, false, 8, false>(p, plan, st);
       }
     }
   }
-  if (p.k % 64 == 0) return go(skinny_kernel<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0, false>);
-  return go(skinny_kernel<NW, U, 0, NMAT, OUT_F32, false, FOLD, 0, false>);
+  if (p.k % 64 == 0) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 0, false>(p, plan, st);
+  return launch_instance<NW, U, 0, NMAT, OUT_F32, false, FOLD, 0, false>(p, plan, st);
 }
 
 template <int NW, int U, int NB, int NMAT, bool OUT_F32>

@@ -31,6 +31,8 @@ built library every entry point raises (there is no CPU implementation).
 from __future__ import annotations
 
 import ctypes
+import functools
+from collections import OrderedDict
 
 import torch
 import torch.nn.functional as F
@@ -121,31 +123,60 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr() if t is not None and t.numel() else 0)
 
 
-# split-K workspaces: one per (device, stream), so that the calls sharing one
-# are ordered by their stream
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-_ws_need: dict[tuple, int] = {}
+# Workspaces of the K-split plans (pair slots that must start empty, then
+# partial tiles):
+#  * eager calls use one buffer per (device, stream), zero-filled when it is
+#    allocated; every call leaves its pair slots empty, so the stream's later
+#    calls reuse it; a larger need replaces it (the old buffer is freed in
+#    stream order, which torch's caching allocator makes safe);
+#  * calls under HIP graph capture use one buffer per capture (device, stream,
+#    capture id), allocated and zero-filled inside the capture: the fill is a
+#    node of that graph, so every replay starts from empty slots whatever used
+#    the memory between replays (graphs sharing a memory pool), and no eager
+#    call shares it.  It is a temporary of the graph's memory pool and leaves
+#    this table once its capture is over.
+_MAX_EAGER_WS = 16  # (device, stream) pairs kept; the least recently used is dropped
+_eager_ws: "OrderedDict[tuple[int, int], torch.Tensor]" = OrderedDict()
+_capture_ws: dict[tuple[int, int], tuple[int, torch.Tensor]] = {}
+_MIN_WS = 4 << 20
+
+
+@functools.lru_cache(maxsize=4096)
+def _ws_need(m: int, ns: tuple, k: int, swiglu: bool, norm: bool) -> int:
+    lib = _native.load()
+    arr = (ctypes.c_int64 * len(ns))(*ns)
+    query = lib.pgs_w8a16_rmsnorm_workspace_bytes if norm else lib.pgs_w8a16_workspace_bytes
+    return int(query(m, arr, len(ns), k, int(swiglu)))
+
+
+def _zeroed(size: int, dev: torch.device) -> torch.Tensor:
+    ws = torch.zeros(size, dtype=torch.uint8, device=dev)  # a fill kernel, capturable
+    if ws.data_ptr() % 256:
+        raise RuntimeError("pageserve_amd: workspace allocation is not 256-byte aligned")
+    return ws
 
 
 def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, swiglu: bool, norm: bool = False):
-    key = (m, ns, k, swiglu, norm)
-    need = _ws_need.get(key)
-    if need is None:
-        arr = (ctypes.c_int64 * len(ns))(*ns)
-        query = lib.pgs_w8a16_rmsnorm_workspace_bytes if norm else lib.pgs_w8a16_workspace_bytes
-        need = int(query(m, arr, len(ns), k, int(swiglu)))
-        _ws_need[key] = need
+    need = _ws_need(m, ns, k, bool(swiglu), bool(norm))
     if need == 0:
         return ctypes.c_void_p(0), 0
-    wkey = (dev.index, stream)
-    ws = _workspaces.get(wkey)
-    if ws is None or ws.numel() < need:
-        size = max(need, 2 * ws.numel() if ws is not None else 0, 4 << 20)
-        # zero-filled: the leading pair slots must start empty (calls leave them empty)
-        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
-        if ws.data_ptr() % 256:
-            raise RuntimeError("pageserve_amd: workspace allocation is not 256-byte aligned")
-        _workspaces[wkey] = ws
+    key = (dev.index, stream)
+    capturing, cid = _native.capture_state(stream)
+    if capturing:
+        cur = _capture_ws.get(key)
+        if cur is None or cur[0] != cid or cur[1].numel() < need:
+            grow = 2 * cur[1].numel() if cur is not None and cur[0] == cid else 0
+            _capture_ws[key] = (cid, _zeroed(max(need, grow, _MIN_WS), dev))
+        ws = _capture_ws[key][1]
+    else:
+        _capture_ws.pop(key, None)  # that capture is over
+        ws = _eager_ws.get(key)
+        if ws is None or ws.numel() < need:
+            ws = _zeroed(max(need, 2 * ws.numel() if ws is not None else 0, _MIN_WS), dev)
+            _eager_ws[key] = ws
+            while len(_eager_ws) > _MAX_EAGER_WS:
+                _eager_ws.popitem(last=False)
+        _eager_ws.move_to_end(key)
     return ctypes.c_void_p(ws.data_ptr()), ws.numel()
 
 

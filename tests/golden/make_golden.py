@@ -1,4 +1,4 @@
-"""Writes tests/golden/config1_gate_proj.npz: a fixture for the single-linear
+"""Writes tests/golden/gate_proj_4864x896.npz: a fixture for the single-linear
 case (Qwen2.5-0.5B gate_proj shape): W fp32 [4864, 896] ~ N(0, 0.02), x bf16
 [1, 896] ~ N(0, 1), quantized per output row and y = x (q s)^T.
 
@@ -30,7 +30,7 @@ import exact  # noqa: E402
 
 N, K, M = 4864, 896, 1
 W_SEED, X_SEED, ROW_SEED = 20240, 20241, 20242
-PATH = os.path.join(HERE, "config1_gate_proj.npz")
+PATH = os.path.join(HERE, "gate_proj_4864x896.npz")
 
 
 def inputs():

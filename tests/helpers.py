@@ -32,8 +32,22 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy()
 
 
-def report(y: np.ndarray, y_ref: np.ndarray, k: int, what: str, bf16_out: bool = True, ulp_of=None) -> dict:
-    """Asserts the specification's tolerance (oracle.compare) and returns the report."""
-    r = O.compare(y, y_ref, k, bf16_out=bf16_out, ulp_of=ulp_of)
+def report(y: np.ndarray, y_ref: np.ndarray, k: int, what: str, bf16_out: bool = True, ulp_of=None,
+           acc=None) -> dict:
+    """Asserts the specification's tolerance (oracle.compare) and returns the
+    report.  ``acc``: the elementwise accumulation bound of a bf16 output
+    (O.acc_bound / O.swiglu_acc of the same inputs)."""
+    r = O.compare(y, y_ref, k, bf16_out=bf16_out, ulp_of=ulp_of, acc=acc)
     assert r["ok"], f"{what}: {r}"
     return r
+
+
+def linear_ref(x: np.ndarray, q: np.ndarray, s: np.ndarray, b: np.ndarray | None = None) -> dict:
+    """Oracle output and accumulation bound of a linear, as report() keywords:
+    ``report(y, **linear_ref(x, q, s, b), k=..., what=...)``."""
+    return {"y_ref": O.linear(x, q, s, b), "acc": O.acc_bound(x, q, s, b)}
+
+
+def swiglu_ref(x: np.ndarray, qg, sg, qu, su) -> dict:
+    """Oracle output and accumulation bound of the SwiGLU pair."""
+    return {"y_ref": O.swiglu(x, qg, sg, qu, su), "acc": O.swiglu_acc(x, qg, sg, qu, su)}

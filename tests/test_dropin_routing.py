@@ -79,40 +79,49 @@ def test_metadata_reads_do_not_materialise():
     assert qw.calls == []
 
 
-def test_compare_floors_bf16_outputs_at_one_ulp():
+def test_compare_floors_bf16_outputs_at_half_an_ulp():
     ref = np.array([10.0, 0.5, -3.0], dtype=np.float32)
-    # one bf16 ulp at 10.0 is 0.0625 > 2e-2*sqrt(2): allowed only for a bf16 output
-    y = ref + np.array([0.0625, 0.0, 0.0], dtype=np.float32)
+    # half a bf16 ulp at 10.0 is 0.03125 > 2e-2*sqrt(2): allowed only for a bf16 output
+    y = ref + np.array([0.03125, 0.0, 0.0], dtype=np.float32)
     assert not O.compare(y, ref, 2048)["ok"]
-    assert O.compare(y, ref, 2048, bf16_out=True)["ok"]
-    y2 = ref + np.array([0.13, 0.0, 0.0], dtype=np.float32)
-    assert not O.compare(y2, ref, 2048, bf16_out=True)["ok"]
+    assert O.compare(y, ref, 2048, bf16_out=True, acc=0.0)["ok"]
+    # a whole ulp is a wrong rounding, not a rounding of the right value
+    y1 = ref + np.array([0.0625, 0.0, 0.0], dtype=np.float32)
+    assert not O.compare(y1, ref, 2048, bf16_out=True, acc=0.0)["ok"]
+    # the accumulation bound widens the floor elementwise, and only by itself
+    y2 = ref + np.array([0.04, 0.0, 0.0], dtype=np.float32)
+    assert O.compare(y2, ref, 2048, bf16_out=True, acc=np.array([0.01, 0.0, 0.0]))["ok"]
+    assert not O.compare(y2, ref, 2048, bf16_out=True, acc=np.array([0.005, 0.0, 0.0]))["ok"]
     # small values keep the specification's absolute bound
     y3 = ref + np.array([0.0, 0.03, 0.0], dtype=np.float32)
-    assert not O.compare(y3, ref, 2048, bf16_out=True)["ok"]
+    assert not O.compare(y3, ref, 2048, bf16_out=True, acc=0.0)["ok"]
+    # a single-rounding bf16 comparison must state its accumulation bound
+    with pytest.raises(ValueError, match="accumulation bound"):
+        O.compare(y, ref, 2048, bf16_out=True)
 
 
 def test_compare_floor_across_a_power_of_two_and_for_a_rounded_intermediate():
-    # reference just below 1.0 (ulp 2^-8), result 1.0: one ulp of the upper
-    # binade apart, which a K = 128 bound (0.00707) cannot resolve
-    ref = np.array([1 - 2 ** -7, 0.25], dtype=np.float32)
-    y = np.array([1.0, 0.25], dtype=np.float32)
-    assert O.compare(y, ref, 128, bf16_out=True)["ok"]
-    assert not O.compare(np.array([1 + 2 ** -7, 0.25], np.float32), ref, 128, bf16_out=True)["ok"]
+    # reference just below 8.0 (bf16 spacing 2^-5 there), result 8.0 (the fp32
+    # sum landed on the other side of the midpoint): a quarter ulp of the upper
+    # binade apart, which a K = 16 bound (0.005) cannot resolve; the next bf16
+    # value above 8 is a wrong rounding
+    ref = np.array([8 - 2 ** -6, 0.25], dtype=np.float32)
+    assert O.compare(np.array([8.0, 0.25], np.float32), ref, 16, bf16_out=True, acc=0.0)["ok"]
+    assert not O.compare(np.array([8.0625, 0.25], np.float32), ref, 16, bf16_out=True, acc=0.0)["ok"]
     # residual + bf16(linear) cancelling to a small sum: a one-ulp step of the
     # intermediate (3.0 -> ulp 2^-6) is allowed only when the intermediate is given
     # (a second element of typical size keeps the relative bound, max|dy| / max|ref|, out of the way)
     ref2 = np.array([0.1015625, 4.0], dtype=np.float32)
     inter = np.array([3.0, 1.0])
     step = np.array([2 ** -6, 0.0], dtype=np.float32)
-    assert not O.compare(ref2 + step, ref2, 128, bf16_out=True)["ok"]
+    assert not O.compare(ref2 + step, ref2, 128, bf16_out=True, acc=0.0)["ok"]
     assert O.compare(ref2 + step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
     assert not O.compare(ref2 + 2 * step, ref2, 128, bf16_out=True, ulp_of=inter)["ok"]
     # intermediate and result of similar size: the flip and the final rounding add up
     ref3 = np.array([1.5, 4.0], dtype=np.float32)
     inter3 = np.array([1.25, 1.0])
     step3 = np.array([2 ** -6, 0.0], dtype=np.float32)   # = ulp(1.25) + ulp(1.5)
-    assert not O.compare(ref3 + step3, ref3, 48, bf16_out=True)["ok"]
+    assert not O.compare(ref3 + step3, ref3, 48, bf16_out=True, acc=0.0)["ok"]
     assert O.compare(ref3 + step3, ref3, 48, bf16_out=True, ulp_of=inter3)["ok"]
     assert not O.compare(ref3 + 2 * step3, ref3, 48, bf16_out=True, ulp_of=inter3)["ok"]
 

@@ -1,4 +1,4 @@
-"""The committed config-1 fixture (tests/golden/config1_gate_proj.npz, made by
+"""The committed 4864x896 gate_proj fixture (tests/golden/gate_proj_4864x896.npz, made by
 tests/golden/make_golden.py): W fp32 [4864, 896] ~ N(0, 0.02), x bf16 [1, 896].
 
 CPU: the oracle regenerates the fixture from its seeds (full q and scale by
@@ -38,7 +38,7 @@ def _sha(a: np.ndarray) -> np.ndarray:
     return np.frombuffer(hashlib.sha256(np.ascontiguousarray(a).tobytes()).digest(), dtype=np.uint8)
 
 
-def test_fixture_describes_config_1(fixture):
+def test_fixture_describes_the_4864x896_linear(fixture):
     assert tuple(fixture["shape"]) == (G.N, G.K, G.M) == (4864, 896, 1)
     assert tuple(fixture["seeds"]) == (G.W_SEED, G.X_SEED, G.ROW_SEED)
     assert np.array_equal(fixture["rows"], G.sample_rows())
@@ -76,4 +76,5 @@ def test_gpu_reproduces_the_fixture(gpu, fixture):
     assert np.array_equal(_sha(qw.q.cpu().numpy()), fixture["q_sha256"])
     xt = torch.from_numpy(O.f32_to_bf16_bits(x).view(np.int16).copy()).view(torch.bfloat16).to(gpu)
     y = qw.linear(xt)
-    report(y.float().cpu().numpy(), fixture["y"], G.K, "config 1 linear vs fixture")
+    report(y.float().cpu().numpy(), fixture["y"], G.K, "4864x896 linear vs fixture",
+           acc=O.acc_bound(x, *O.quantize_per_channel(w)))

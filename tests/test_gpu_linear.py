@@ -67,14 +67,14 @@ def test_linear_matches_oracle(gpu, m, n, k):
     qw, q, s, x, _ = _problem(gpu, 100 + m + n + k, m, n, k)
     y = qw.linear(bf16_gpu(x, gpu))
     assert y.dtype == torch.bfloat16 and y.shape == (m, n)
-    report(to_np(y), O.linear(x, q, s), k, f"linear m={m} n={n} k={k}")
+    report(to_np(y), O.linear(x, q, s), k, f"linear m={m} n={n} k={k}", acc=O.acc_bound(x, q, s))
 
 
 @pytest.mark.parametrize("m", [1, 3, 16, 24, 40, 256])
 def test_linear_with_bias(gpu, m):
     qw, q, s, x, b = _problem(gpu, 7 + m, m, 2048, 2048, bias=True)
     y = qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu))
-    report(to_np(y), O.linear(x, q, s, b), 2048, f"linear+bias m={m}")
+    report(to_np(y), O.linear(x, q, s, b), 2048, f"linear+bias m={m}", acc=O.acc_bound(x, q, s, b))
 
 
 @pytest.mark.parametrize("m", [1, 8, 20, 32, 256])
@@ -108,8 +108,11 @@ def test_grouped_qkv_matches_separate_calls(gpu, m):
     outs = Q.linear_group(xs, ws, bt)
     for j in range(3):
         single = ws[j].linear(xs, bt[j])
-        report(to_np(outs[j]), O.linear(x, qs[j], ss[j], bs[j]), k, f"qkv[{j}] m={m}")
-        report(to_np(outs[j]), to_np(single), k, f"qkv[{j}] m={m} group vs single")
+        report(to_np(outs[j]), O.linear(x, qs[j], ss[j], bs[j]), k, f"qkv[{j}] m={m}", acc=O.acc_bound(x, qs[j], ss[j], bs[j]))
+        # two correctly rounded results of the same value in different
+        # summation orders: within one ulp plus both accumulation bounds
+        report(to_np(outs[j]), to_np(single), k, f"qkv[{j}] m={m} group vs single",
+               acc=0.5 * O.bf16_ulp(to_np(single)) + 2 * O.acc_bound(x, qs[j], ss[j], bs[j]))
 
 
 def test_leading_dims_and_noncontiguous_input(gpu):
@@ -117,10 +120,10 @@ def test_leading_dims_and_noncontiguous_input(gpu):
     xt = bf16_gpu(x, gpu).reshape(2, 3, 256)
     y = qw.linear(xt)
     assert y.shape == (2, 3, 512)
-    report(to_np(y.reshape(6, 512)), O.linear(x, q, s), 256, "3-D input")
+    report(to_np(y.reshape(6, 512)), O.linear(x, q, s), 256, "3-D input", acc=O.acc_bound(x, q, s))
     # a transposed view: the wrapper copies it to a contiguous buffer
     xT = bf16_gpu(np.ascontiguousarray(x.T), gpu).t()
-    report(to_np(qw.linear(xT)), O.linear(x, q, s), 256, "non-contiguous input")
+    report(to_np(qw.linear(xT)), O.linear(x, q, s), 256, "non-contiguous input", acc=O.acc_bound(x, q, s))
 
 
 def test_full_size_prefill_sampled(gpu):
@@ -133,7 +136,7 @@ def test_full_size_prefill_sampled(gpu):
     rows = rng.choice(m, 96, replace=False)
     cols = rng.choice(n, 512, replace=False)
     ref = O.linear(x[rows], q[cols], s[cols])
-    report(y[np.ix_(rows, cols)], ref, k, "m=2048 sample")
+    report(y[np.ix_(rows, cols)], ref, k, "m=2048 sample", acc=O.acc_bound(x[rows], q[cols], s[cols]))
     assert np.isfinite(y).all()
 
 
@@ -148,7 +151,7 @@ def test_wide_matrix_128_token_tiles_sampled(gpu):
     rows = np.concatenate([rng.choice(m, 60, replace=False), [0, 255, 256, m - 1]])
     cols = np.concatenate([rng.choice(n, 400, replace=False), [0, 127, 128, n - 1]])
     ref = O.linear(x[rows], q[cols], s[cols], b[cols])
-    report(y[np.ix_(rows, cols)], ref, k, "128-token tiles sample")
+    report(y[np.ix_(rows, cols)], ref, k, "128-token tiles sample", acc=O.acc_bound(x[rows], q[cols], s[cols], b[cols]))
     assert np.isfinite(y).all()
 
 
@@ -164,10 +167,12 @@ def test_paired_split_leaves_the_workspace_clean(gpu):
                         (17, 1000, 1040)])]
     xs = [bf16_gpu(c[3], gpu) for c in cases]
     refs = [O.linear(c[3], c[1], c[2]) for c in cases]
+    accs = [O.acc_bound(c[3], c[1], c[2]) for c in cases]
     for rep in range(3):
         outs = [c[0].linear(x) for c, x in zip(cases, xs)]
-        for (qw, q, s, x, _), y, ref in zip(cases, outs, refs):
-            report(to_np(y), ref, x.shape[1], f"paired m={x.shape[0]} n={q.shape[0]} k={x.shape[1]} rep={rep}")
+        for (qw, q, s, x, _), y, ref, acc in zip(cases, outs, refs, accs):
+            report(to_np(y), ref, x.shape[1], f"paired m={x.shape[0]} n={q.shape[0]} k={x.shape[1]} rep={rep}",
+                   acc=acc)
 
 
 @pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48),
@@ -186,7 +191,7 @@ def test_nonfinite_token_stays_in_its_row(gpu, m, n, k):
     ok = [t for t in range(m) if t != bad]
     assert not np.isfinite(y[bad]).any()
     ref = O.linear(x[ok], q, s)
-    report(y[ok], ref, k, f"non-finite token m={m} n={n} k={k}")
+    report(y[ok], ref, k, f"non-finite token m={m} n={n} k={k}", acc=O.acc_bound(x[ok], q, s))
 
 
 def test_deterministic(gpu):
@@ -230,10 +235,10 @@ def test_launch_stream_and_cached_operands(gpu):
         assert _raw_stream(gpu) == side.cuda_stream
     qw, q, s, x, _ = _problem(gpu, 5, 3, 256, 512)
     xt = bf16_gpu(x, gpu)
-    report(to_np(qw.linear(xt)), O.linear(x, q, s), 512, "before")
+    report(to_np(qw.linear(xt)), O.linear(x, q, s), 512, "before", acc=O.acc_bound(x, q, s))
     q2 = np.ascontiguousarray(q[::-1])
     qw.q = torch.from_numpy(q2).to(gpu)
-    report(to_np(qw.linear(xt)), O.linear(x, q2, s), 512, "after assigning q")
+    report(to_np(qw.linear(xt)), O.linear(x, q2, s), 512, "after assigning q", acc=O.acc_bound(x, q2, s))
 
 
 def test_calls_from_a_worker_thread(gpu):
@@ -266,3 +271,47 @@ def test_calls_from_a_worker_thread(gpu):
     assert not t.is_alive() and not errs, errs
     assert torch.equal(out["y"], main)
     assert torch.equal(out["g"], Q.swiglu(xt, qw, qw))
+
+
+def _plan_kernel() -> str:
+    from pageserve_amd import _native
+
+    return _native.last_plan()
+
+
+def test_four_k_group_plan(gpu):
+    """The 256-tile, long-K plan (four K groups of four waves per
+    workgroup, launch_k64<64, 128, 1, *, 2, 2, 1, 4>): down_proj's shape at
+    1024 tokens (256 tiles, no split), and a few-tile long-K shape with a
+    workspace (K split 8 plus the reduce kernel) and without one (the C ABI
+    with a NULL workspace: no split)."""
+    import ctypes
+
+    from pageserve_amd import _native
+
+    kg4 = "BM = 64, BN = 128, NMAT = 1, OUT_F32 = false, WLEAD = 2, XLEAD = 2, OCC = 1, KG = 4"
+    m, n, k = 1024, 2048, 11008
+    qw, q, s, x, _ = _problem(gpu, 7711, m, n, k)
+    y = to_np(qw.linear(bf16_gpu(x, gpu)))
+    assert kg4 in _plan_kernel() and "splits=1" in _plan_kernel(), _plan_kernel()
+    rows = np.concatenate([np.random.default_rng(3).choice(m, 40, replace=False), [0, 63, 64, m - 1]])
+    report(y[rows], O.linear(x[rows], q, s), k, "kg4 m=1024", acc=O.acc_bound(x[rows], q, s))
+
+    m, n, k = 200, 200, 4160
+    qw, q, s, x, b = _problem(gpu, 7712, m, n, k, bias=True)
+    xt, bt = bf16_gpu(x, gpu), bf16_gpu(b, gpu)
+    y = to_np(qw.linear(xt, bt))
+    plan = _plan_kernel()
+    assert kg4 in plan and "splits=8" in plan and "gemm_reduce_kernel" in plan, plan
+    report(y, O.linear(x, q, s, b), k, "kg4 split", acc=O.acc_bound(x, q, s, b))
+    lib = _native.load()
+    qp, sc = qw._kernel_operands()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.pgs_w8a16_linear(ctypes.c_void_p(xt.data_ptr()), ctypes.c_void_p(qp.data_ptr()),
+                              ctypes.c_void_p(sc.data_ptr()), ctypes.c_void_p(bt.data_ptr()),
+                              ctypes.c_void_p(out.data_ptr()), 1, m, n, k, None, 0, ctypes.c_void_p(stream))
+    assert rc == 0, lib.pgs_last_error()
+    plan = _plan_kernel()
+    assert kg4 in plan and "splits=1" in plan, plan
+    report(to_np(out), O.linear(x, q, s, b), k, "kg4 no workspace", acc=O.acc_bound(x, q, s, b))

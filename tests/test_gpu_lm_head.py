@@ -28,18 +28,29 @@ def lm_head(gpu):
     return qw, q, s
 
 
+def _oracle_blocked(x: np.ndarray, q: np.ndarray, s: np.ndarray, block: int = 16384) -> np.ndarray:
+    """O.linear over the vocabulary in blocks of rows (the float64 dequantized
+    weight of one block at a time stays a few hundred MB)."""
+    return np.concatenate([O.linear(x, q[i:i + block], s[i:i + block]) for i in range(0, q.shape[0], block)], axis=1)
+
+
 @pytest.mark.parametrize("m", [1, 8, 256])
 def test_lm_head_logits_and_argmax(gpu, lm_head, m):
+    """Every row: fp32 logits within the tolerance of the oracle's, and the
+    argmax (server.py:51 takes it) equal to the oracle's; rows whose top two
+    oracle logits are too close to decide are reported, not skipped."""
     qw, q, s = lm_head
     x = activations(77 + m, m, HIDDEN)
     logits = qw.linear(bf16_gpu(x, gpu), out_dtype=torch.float32)
     assert logits.dtype == torch.float32 and logits.shape == (m, VOCAB)
     got = to_np(logits)
-    rows = np.arange(m) if m <= 8 else np.random.default_rng(m).choice(m, 24, replace=False)
-    ref = O.linear(x[rows], q, s)
-    report(got[rows], ref, HIDDEN, f"lm_head m={m}", bf16_out=False)
+    ref = _oracle_blocked(x, q, s)
+    report(got, ref, HIDDEN, f"lm_head m={m}", bf16_out=False)
     gap = O.top2_gap(ref)
-    assert (gap > 1e-4).all(), f"near-tie in the oracle, argmax not decidable: {gap.min()}"
-    np.testing.assert_array_equal(O.argmax_rows(got[rows]), O.argmax_rows(ref))
-    # every row's argmax via the GPU's own argmax as the serving loop takes it
-    assert torch.equal(logits.argmax(dim=-1).cpu(), torch.from_numpy(O.argmax_rows(got)))
+    # the kernel's fp32 logits sit within the accumulation bound of the exact
+    # ones: a gap above twice the largest bound decides the argmax
+    worst = float(np.abs(got - ref).max())
+    assert (gap > 2 * worst).all(), f"near-tie in the oracle: gap {gap.min()} vs error {worst}"
+    np.testing.assert_array_equal(O.argmax_rows(got), O.argmax_rows(ref))
+    # and through torch's own argmax on the GPU, as the serving loop takes it
+    np.testing.assert_array_equal(logits.argmax(dim=-1).cpu().numpy(), O.argmax_rows(ref))

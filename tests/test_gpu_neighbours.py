@@ -111,13 +111,14 @@ def test_decode_layer_neighbours_chain(gpu):
     x2 = Q.mlp(h2, qw["g"], qw["u"], qw["d"], residual=x1)
     # oracle chain (fed with the kernel's own intermediate where rounding
     # boundaries could otherwise diverge by one ulp)
-    h_ref = O.rmsnorm(x, ln1, 1e-6)
     for j, nm in enumerate("qkv"):
-        report(to_np(qkv[j]), O.linear(to_np(h), *qs[nm]), H, f"layer {nm}")
-    report(to_np(h), h_ref, H, "layer rmsnorm 1")
+        report(to_np(qkv[j]), O.linear(to_np(h), *qs[nm]), H, f"layer {nm}", acc=O.acc_bound(to_np(h), *qs[nm]))
+    lo, hi = O.rmsnorm_bracket(x, ln1, 1e-6)
+    assert ((lo <= to_np(h)) & (to_np(h) <= hi)).all(), "layer rmsnorm 1 outside the oracle's bracket"
     report(to_np(x1), O.linear_residual(a, *qs["o"], x), H, "layer o + residual",
            ulp_of=O.linear_residual_intermediate(a, *qs["o"]))
-    report(to_np(h2), O.rmsnorm(to_np(x1), ln2, 1e-6), H, "layer rmsnorm 2")
+    lo, hi = O.rmsnorm_bracket(to_np(x1), ln2, 1e-6)
+    assert ((lo <= to_np(h2)) & (to_np(h2) <= hi)).all(), "layer rmsnorm 2 outside the oracle's bracket"
     act = O.swiglu(to_np(h2), *qs["g"], *qs["u"])
     report(to_np(x2), O.linear_residual(O.round_to_bf16(act), *qs["d"], to_np(x1)), I, "layer down + residual",
            ulp_of=O.linear_residual_intermediate(O.round_to_bf16(act), *qs["d"]))

@@ -216,3 +216,28 @@ def test_random_quantize_bit_exact(gpu, i):
         torch.from_numpy(O.f32_to_bf16_bits(w).view(np.int16).copy()).view(torch.bfloat16).to(gpu)
     qw = Q.QuantizedWeight(wt)
     _assert_bit_exact(qw.q.cpu().numpy(), qw.scale.cpu().numpy(), q_ref, s_ref, f"packed case {i} [{n},{k}] {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_non_finite_rows_follow_the_reference(gpu, dtype):
+    """A row holding a NaN gets a NaN scale, a row holding an infinity an
+    infinite scale, and every NaN quotient q = 0 (the reference's torch CPU
+    arithmetic, pinned in the oracle tests); other rows are unaffected."""
+    w = random_matrix(77, 8, 192)
+    w[1, 7] = np.nan
+    w[2, 3] = np.inf
+    w[3, 0] = -np.inf
+    w[4, 9], w[4, 100] = np.nan, np.inf
+    if dtype == torch.bfloat16:
+        w = O.round_to_bf16(w)
+    q, s = _gpu_quant(w, gpu, dtype)
+    q_ref, s_ref = O.quantize_per_channel(w)
+    np.testing.assert_array_equal(q, q_ref)
+    np.testing.assert_array_equal(np.isnan(s), np.isnan(s_ref))
+    fin = ~np.isnan(s_ref)
+    np.testing.assert_array_equal(s[fin].view(np.uint32), s_ref[fin].view(np.uint32))
+    assert np.isnan(s[1, 0]) and np.isnan(s[4, 0]) and np.isinf(s[2, 0]) and np.isinf(s[3, 0])
+    # the packed store agrees
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu) if dtype == torch.float32 else
+                           torch.from_numpy(O.f32_to_bf16_bits(w).view(np.int16).copy()).view(torch.bfloat16).to(gpu))
+    np.testing.assert_array_equal(qw.q.cpu().numpy(), q_ref)

@@ -60,7 +60,7 @@ def test_random_shape(gpu, i):
         qws = [Q.QuantizedWeight(torch.from_numpy(w).to(gpu)) for w in ws]
         ys = Q.linear_group(xt, qws, [bf16_gpu(b, gpu) if b is not None else None for b in bs])
         for j, (w, b, y) in enumerate(zip(ws, bs, ys)):
-            report(to_np(y), O.linear(x, *O.quantize_per_channel(w), b), k, f"{what} member {j}")
+            report(to_np(y), O.linear(x, *O.quantize_per_channel(w), b), k, f"{what} member {j}", acc=O.acc_bound(x, *O.quantize_per_channel(w), b))
         return
     w = weights(23_000 + i, n, k)
     q, s = O.quantize_per_channel(w)
@@ -68,7 +68,7 @@ def test_random_shape(gpu, i):
     if kind == "swiglu":
         w2 = weights(24_000 + i, n, k)
         act = Q.swiglu(xt, qw, Q.QuantizedWeight(torch.from_numpy(w2).to(gpu)))
-        report(to_np(act), O.swiglu(x, q, s, *O.quantize_per_channel(w2)), k, what)
+        report(to_np(act), O.swiglu(x, q, s, *O.quantize_per_channel(w2)), k, what, acc=O.swiglu_acc(x, q, s, *O.quantize_per_channel(w2)))
         return
     b = O.round_to_bf16(np.random.default_rng(25_000 + i).standard_normal(n).astype(np.float32)) if bias else None
     bt = bf16_gpu(b, gpu) if bias else None
@@ -78,7 +78,7 @@ def test_random_shape(gpu, i):
         report(to_np(y), O.linear_residual(x, q, s, r, b), k, what, ulp_of=O.linear_residual_intermediate(x, q, s, b))
     else:
         y = qw.linear(xt, bt)
-        report(to_np(y), O.linear(x, q, s, b), k, what)
+        report(to_np(y), O.linear(x, q, s, b), k, what, acc=O.acc_bound(x, q, s, b))
 
 
 # rms_norm fused into the projections (engine/model.py:166-170, 187-189):
@@ -107,7 +107,7 @@ def test_random_fused_norm(gpu, i):
     # entries whose squares sum exactly in fp32 in any order: fused == unfused bit for bit
     xe = rng.choice(np.array([0.5, -0.5, 1.0, -1.0, 2.0, -2.0], np.float32), size=(m, k))
     xt, xet, wt = bf16_gpu(x, gpu), bf16_gpu(xe, gpu), bf16_gpu(w, gpu)
-    h = O.rmsnorm(x, w, eps)
+    h, dh = O.rmsnorm(x, w, eps), O.rmsnorm_dx(x, w, eps)
     if kind == "group":
         ns = [n, max(1, n // 4)]
         ws = [weights(32_000 + 10 * i + j, nn, k) for j, nn in enumerate(ns)]
@@ -117,7 +117,7 @@ def test_random_fused_norm(gpu, i):
         ys = Q.rmsnorm_linear_group(xt, wt, eps, qws, bts)
         for j, (v, b, y) in enumerate(zip(ws, bs, ys)):
             q, s = O.quantize_per_channel(v)
-            report(to_np(y), O.linear(h, q, s, b), k, f"{what} output {j}")
+            report(to_np(y), O.linear(h, q, s, b), k, f"{what} output {j}", acc=O.acc_bound(h, q, s, b, dx=dh))
         fused = Q.rmsnorm_linear_group(xet, wt, eps, qws, bts)
         plain = Q.linear_group(Q.rmsnorm(xet, wt, eps), qws, bts)
         assert all(torch.equal(a, b) for a, b in zip(fused, plain)), what
@@ -125,6 +125,6 @@ def test_random_fused_norm(gpu, i):
         wg, wu = weights(33_000 + i, n, k), weights(34_000 + i, n, k)
         g, u = Q.QuantizedWeight(torch.from_numpy(wg).to(gpu)), Q.QuantizedWeight(torch.from_numpy(wu).to(gpu))
         act = Q.rmsnorm_swiglu(xt, wt, eps, g, u)
-        ref = O.swiglu(h, *O.quantize_per_channel(wg), *O.quantize_per_channel(wu))
-        report(to_np(act), ref, k, what)
+        qg, qu = O.quantize_per_channel(wg), O.quantize_per_channel(wu)
+        report(to_np(act), O.swiglu(h, *qg, *qu), k, what, acc=O.swiglu_acc(h, *qg, *qu, dx=dh))
         assert torch.equal(Q.rmsnorm_swiglu(xet, wt, eps, g, u), Q.swiglu(Q.rmsnorm(xet, wt, eps), g, u)), what

@@ -75,9 +75,10 @@ def test_rmsnorm_linear_group_matches_oracle(gpu, m, ns, k):
     w = norm_weight(k, k)
     biases = [O.round_to_bf16(rng.standard_normal(n).astype(np.float32)) for n in ns]
     outs = Q.rmsnorm_linear_group(bf16_gpu(x, gpu), bf16_gpu(w, gpu), 1e-6, qws, [bf16_gpu(b, gpu) for b in biases])
-    h = O.rmsnorm(x, w, 1e-6)
+    h, dh = O.rmsnorm(x, w, 1e-6), O.rmsnorm_dx(x, w, 1e-6)
     for j, (q, s) in enumerate(qs):
-        report(to_np(outs[j]), O.linear(h, q, s, biases[j]), k, f"rmsnorm+linear m={m} n={ns[j]} k={k}")
+        report(to_np(outs[j]), O.linear(h, q, s, biases[j]), k, f"rmsnorm+linear m={m} n={ns[j]} k={k}",
+               acc=O.acc_bound(h, q, s, biases[j], dx=dh))
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5])
@@ -90,9 +91,10 @@ def test_rmsnorm_swiglu_equals_unfused_and_oracle(gpu, m, n, k):
     assert torch.equal(Q.rmsnorm_swiglu(xe, w, 1e-6, g, u), Q.swiglu(Q.rmsnorm(xe, w, 1e-6), g, u))
     x = activations(m * 3 + n, m, k)
     act = Q.rmsnorm_swiglu(bf16_gpu(x, gpu), w, 1e-6, g, u)
-    h = O.rmsnorm(x, norm_weight(n, k), 1e-6)
-    ref = O.swiglu(h, *O.quantize_per_channel(wg), *O.quantize_per_channel(wu))
-    report(to_np(act), ref, k, f"rmsnorm+swiglu m={m} n={n} k={k}")
+    h, dh = O.rmsnorm(x, norm_weight(n, k), 1e-6), O.rmsnorm_dx(x, norm_weight(n, k), 1e-6)
+    qg, qu = O.quantize_per_channel(wg), O.quantize_per_channel(wu)
+    report(to_np(act), O.swiglu(h, *qg, *qu), k, f"rmsnorm+swiglu m={m} n={n} k={k}",
+           acc=O.swiglu_acc(h, *qg, *qu, dx=dh))
 
 
 @pytest.mark.parametrize("m", [1, 3])
@@ -176,9 +178,9 @@ def test_zero_rows_eps_and_repeat_calls(gpu):
         assert torch.equal(outs[j], Q.rmsnorm_linear_group(xt, wt, 1e-6, qws, bt)[j])
     x0 = np.delete(x, 1, axis=0)
     outs0 = Q.rmsnorm_linear_group(bf16_gpu(x0, gpu), wt, 0.0, qws)
-    h = O.rmsnorm(x0, w, 0.0)
+    h, dh = O.rmsnorm(x0, w, 0.0), O.rmsnorm_dx(x0, w, 0.0)
     for j, (q, s) in enumerate(qs):
-        report(to_np(outs0[j]), O.linear(h, q, s), k, f"eps=0 output {j}")
+        report(to_np(outs0[j]), O.linear(h, q, s), k, f"eps=0 output {j}", acc=O.acc_bound(h, q, s, dx=dh))
 
 
 def test_empty_and_bad_norm_weight(gpu):

@@ -41,7 +41,8 @@ def test_swiglu_matches_oracle(gpu, m, inter, hidden):
     act = Q.swiglu(bf16_gpu(x, gpu), ws["gate"][0], ws["up"][0])
     assert act.dtype == torch.bfloat16 and act.shape == (m, inter)
     ref = O.swiglu(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2])
-    report(to_np(act), ref, hidden, f"swiglu m={m}")
+    acc = O.swiglu_acc(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2])
+    report(to_np(act), ref, hidden, f"swiglu m={m}", acc=acc)
 
 
 @pytest.mark.parametrize("m", [1, 512])
@@ -52,7 +53,8 @@ def test_mlp_config(gpu, m):
     x = activations(4100 + m, m, 2048)
     out = Q.mlp(bf16_gpu(x, gpu), ws["gate"][0], ws["up"][0], ws["down"][0])
     ref = O.mlp(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2], ws["down"][1], ws["down"][2])
-    report(to_np(out), ref, 11008, f"mlp m={m}")
+    report(to_np(out), ref, 11008, f"mlp m={m}", acc=O.mlp_acc(x, ws["gate"][1], ws["gate"][2], ws["up"][1],
+                                                              ws["up"][2], ws["down"][1], ws["down"][2]))
 
 
 def test_swiglu_equals_unfused_composition(gpu):

@@ -133,3 +133,52 @@ def test_rmsnorm_workspace_query(native_lib):
                                         (-1, 4, -1)])
 def test_packed_bytes(native_lib, n, k, expect):
     assert native_lib.pgs_packed_bytes(n, k) == expect
+
+
+def _has_gpu() -> bool:
+    try:
+        import torch
+
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+@pytest.mark.parametrize(
+    "call",
+    [
+        lambda L: L.pgs_rmsnorm(ctypes.c_void_p(256), ctypes.c_void_p(256), 1e-6, ctypes.c_void_p(512), 1, 16, None),
+        lambda L: L.pgs_w8a16_linear(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), None,
+                                     ctypes.c_void_p(256), 1, 1, 16, 64, None, 0, None),
+        lambda L: L.pgs_quantize_per_channel(ctypes.c_void_p(256), 0, 4, 64, ctypes.c_void_p(256),
+                                             ctypes.c_void_p(256), None),
+        lambda L: L.pgs_pack_weight(ctypes.c_void_p(256), 4, 64, ctypes.c_void_p(256), None),
+    ],
+)
+def test_no_device_is_an_error_not_a_launch(native_lib, call):
+    """Well-formed calls on a machine without a (gfx950) device return
+    PGS_ERR_NO_DEVICE before launching anything."""
+    if _has_gpu():
+        pytest.skip("a GPU is visible: the device check passes there")
+    assert call(native_lib) == 4
+    assert b"device" in native_lib.pgs_last_error()
+
+
+def test_last_plan_is_empty_before_any_launch(native_lib):
+    import threading
+
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(native_lib.pgs_last_plan()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+
+
+def test_capture_state_arguments(native_lib):
+    assert native_lib.pgs_stream_capture_state(None, None, None) == 1
+    cap, cid = ctypes.c_int(7), ctypes.c_ulonglong(7)
+    rc = native_lib.pgs_stream_capture_state(None, ctypes.byref(cap), ctypes.byref(cid))
+    if rc == 0:
+        assert (cap.value, cid.value) == (0, 0)  # the null stream is not capturing
+    else:
+        assert rc == 4 and not _has_gpu()

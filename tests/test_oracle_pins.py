@@ -383,3 +383,97 @@ def test_packed_layout_round_trip_and_padding(n, k):
         for j in range(k):
             covered[((r // 16) * tk + j // 64) * 1024 + ((r % 16) + 16 * ((j % 64) // 16)) * 16 + j % 16] = True
     assert (p[~covered] == 0).all() and covered.sum() == n * k
+
+
+# ---------------------------------------------------------------------------
+# 5. non-finite weights: the reference's op sequence in torch on the CPU (an
+#    independent implementation of engine/quantization.py:20-22) gives a NaN
+#    scale to a row holding a NaN, an infinite scale to a row holding an
+#    infinity, and q = 0 wherever the quotient is NaN
+# ---------------------------------------------------------------------------
+
+def test_quantizer_non_finite_rows_follow_torch_cpu():
+    torch = pytest.importorskip("torch")
+    w = random_matrix(41, 6, 96)
+    w[1, 7] = np.nan
+    w[2, 3] = np.inf
+    w[3, 0] = -np.inf
+    w[4, 9], w[4, 10] = np.nan, np.inf
+    t = torch.from_numpy(w)
+    absmax = t.float().abs().amax(dim=1, keepdim=True).clamp(min=1e-8)
+    scale = absmax / 127.0
+    q = torch.clamp((t.float() / scale).round(), -127, 127).to(torch.int8)
+    oq, os_ = O.quantize_per_channel(w)
+    np.testing.assert_array_equal(oq, q.numpy())
+    np.testing.assert_array_equal(np.isnan(os_), np.isnan(scale.numpy()))
+    fin = ~np.isnan(os_)
+    np.testing.assert_array_equal(os_[fin].view(np.uint32), scale.numpy()[fin].view(np.uint32))
+    assert np.isnan(os_[1, 0]) and np.isnan(os_[4, 0]) and np.isinf(os_[2, 0]) and np.isinf(os_[3, 0])
+    assert (oq[1:5] == 0).all() and (oq[5] != 0).any()
+
+
+# ---------------------------------------------------------------------------
+# 6. the accumulation bound of the bf16 tolerance (O.acc_bound, O.swiglu_acc)
+#    must hold for fp32 evaluations in any summation order -- including an
+#    input where sequential fp32 addition absorbs every small term -- and a
+#    bound without its factor K must not
+# ---------------------------------------------------------------------------
+
+def _fp32_linear(x, q, s, order):
+    """fp32 evaluation of x (q s)^T: exact fp32 products summed in fp32 in
+    the given order, then one multiply by the scale."""
+    p = (x.astype(np.float32)[:, None, :] * q.astype(np.float32)[None, :, :]).astype(np.float32)
+    if order == "forward":
+        acc = np.add.accumulate(p, axis=-1, dtype=np.float32)[..., -1]
+    elif order == "reverse":
+        acc = np.add.accumulate(p[..., ::-1], axis=-1, dtype=np.float32)[..., -1]
+    else:  # blocks of 32 (an MFMA's k extent) summed in fp32, then the blocks in sequence
+        blocks = p.reshape(p.shape[0], p.shape[1], -1, 32).sum(axis=-1, dtype=np.float32)
+        acc = np.add.accumulate(blocks, axis=-1, dtype=np.float32)[..., -1]
+    return (acc * s.reshape(1, -1)).astype(np.float32)
+
+
+def _acc_inputs():
+    rng = np.random.default_rng(43)
+    k = 4096
+    q, s = O.quantize_per_channel(random_matrix(44, 12, k))
+    x = O.round_to_bf16(rng.standard_normal((3, k)).astype(np.float32))
+    # row 0 of q / token 0 of x: one large product, then K-1 products below
+    # half an fp32 ulp of it, each absorbed by a sequential fp32 sum
+    q[0, :] = 1
+    q[0, 0] = 127
+    x[0, :] = np.float32(2.0 ** -20)
+    x[0, 0] = 1.0
+    return x, q, s
+
+
+@pytest.mark.parametrize("order", ["forward", "reverse", "blocked"])
+def test_accumulation_bound_holds_in_any_order(order):
+    x, q, s = _acc_inputs()
+    exact64 = x.astype(np.float64) @ O.dequantize(q, s, "f32").astype(np.float64).T
+    y32 = _fp32_linear(x, q, s, order)
+    acc = O.acc_bound(x, q, s)
+    assert (np.abs(y32 - exact64) <= acc).all()
+
+
+def test_accumulation_bound_without_k_is_caught():
+    x, q, s = _acc_inputs()
+    exact64 = x.astype(np.float64) @ O.dequantize(q, s, "f32").astype(np.float64).T
+    y32 = _fp32_linear(x, q, s, "forward")
+    k = q.shape[1]
+    mutant = O.acc_bound(x, q, s) * (8.0 / (k + 8))
+    assert (np.abs(y32 - exact64) > mutant).any()
+
+
+def test_swiglu_bound_holds_for_an_fp32_evaluation():
+    rng = np.random.default_rng(45)
+    k = 2048
+    qg, sg = O.quantize_per_channel(random_matrix(46, 16, k))
+    qu, su = O.quantize_per_channel(random_matrix(47, 16, k))
+    x = O.round_to_bf16((rng.standard_normal((4, k)) * 3).astype(np.float32))
+    g = _fp32_linear(x, qg, sg, "forward")
+    u = _fp32_linear(x, qu, su, "reverse")
+    act32 = (g / (np.float32(1) + np.exp(-g, dtype=np.float32)) * u).astype(np.float32)
+    ref = O.swiglu(x, qg, sg, qu, su)
+    bound = O.swiglu_acc(x, qg, sg, qu, su)
+    assert (np.abs(act32.astype(np.float64) - ref) <= bound + np.abs(ref) * 2.0 ** -24).all()
