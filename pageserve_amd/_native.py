@@ -62,6 +62,7 @@ SIGNATURES = {
     "pgs_unpack_weight": (_INT, [_VP, _I64, _I64, _VP, _VP]),
     "pgs_dequantize_packed": (_INT, [_VP, _VP, _I64, _I64, _VP, _INT, _VP]),
     "pgs_w8a16_linear": (_INT, [_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_linear_noalloc": (_INT, [_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP]),
     "pgs_w8a16_linear_group": (_INT, [_VP, ctypes.POINTER(LinearOut), _INT, _INT, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_w8a16_linear_residual": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_rmsnorm": (_INT, [_VP, _VP, ctypes.c_float, _VP, _I64, _I64, _VP]),

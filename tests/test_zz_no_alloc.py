@@ -1,0 +1,84 @@
+"""pgs_w8a16_linear_noalloc, the entry point that allocates nothing: called
+through the C ABI, its outputs equal pgs_w8a16_linear's (same launch plan,
+the workspace taken from the library's fixed device array instead of the
+caller) bit for bit, on two calls in a row, the second with a smaller input,
+for plans that use the scratch (split-K partials, pair slots) and one that
+does not; a call whose plan needs more than the array holds is rejected."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import activations, bf16_gpu, report, to_np, weights
+from oracle import quantization_oracle as O
+from pageserve_amd import _native
+from pageserve_amd import quantization as Q
+
+pytestmark = pytest.mark.gpu
+
+VP = ctypes.c_void_p
+
+
+def _noalloc(lib):
+    return lib.pgs_w8a16_linear_noalloc  # typed by the binding (pageserve_amd._native)
+
+
+def _ptr(t):
+    return VP(t.data_ptr()) if t is not None else None
+
+
+def _reference_call(lib, x, qp, sc, b, y, m, n, k, stream):
+    """pgs_w8a16_linear with a freshly zeroed workspace of the exact size."""
+    need = lib.pgs_w8a16_workspace_bytes(m, (ctypes.c_int64 * 1)(n), 1, k, 0)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device) if need else None
+    rc = lib.pgs_w8a16_linear(_ptr(x), _ptr(qp), _ptr(sc), _ptr(b), _ptr(y), 1, m, n, k,
+                              _ptr(ws) if ws is not None else None, need, VP(stream))
+    assert rc == 0, lib.pgs_last_error()
+    return need
+
+
+# (m, n, k): down_proj at 200 tokens (split-K partials, 16.5 MiB) then o_proj
+# at 9 tokens (pair slots); down_proj at 5 tokens (pair slots) then 1 token
+# (folded, no scratch); a ragged tiled split then a smaller one
+PAIRS = [((200, 2048, 11008), (9, 2048, 2048)), ((5, 2048, 11008), (1, 2048, 11008)),
+         ((150, 300, 4160), (40, 200, 4160))]
+
+
+@pytest.mark.parametrize("first,second", PAIRS)
+def test_noalloc_equals_the_workspace_entry_point(gpu, first, second):
+    lib = _native.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep, (m, n, k) in enumerate((first, second)):
+        w = weights(900 + n + k, n, k)
+        qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu))
+        qp, sc = qw._kernel_operands()
+        x = activations(910 + m, m, k)
+        b = O.round_to_bf16(np.random.default_rng(920 + n).standard_normal(n).astype(np.float32))
+        xt, bt = bf16_gpu(x, gpu), bf16_gpu(b, gpu)
+        y_ref = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+        need = _reference_call(lib, xt, qp, sc, bt, y_ref, m, n, k, stream)
+        plan_ref = _native.last_plan()
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        rc = _noalloc(lib)(_ptr(xt), _ptr(qp), _ptr(sc), _ptr(bt), _ptr(y), 1, m, n, k, VP(stream))
+        assert rc == 0, lib.pgs_last_error()
+        assert _native.last_plan() == plan_ref, (plan_ref, _native.last_plan())
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"call {rep} (m={m} n={n} k={k}, scratch {need} B) differs"
+        rows = np.arange(m) if m <= 16 else np.linspace(0, m - 1, 16).astype(int)
+        q, s = O.quantize_per_channel(w)
+        report(to_np(y)[rows], O.linear(x[rows], q, s, b), k, f"noalloc m={m}", acc=O.acc_bound(x[rows], q, s, b))
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch(gpu):
+    lib = _native.load()
+    # find a shape whose split plan needs more than the fixed 32 MiB
+    m, n, k = 960, 2176, 32768  # 255 tiles, K split 8: 64.25 MiB
+    need = lib.pgs_w8a16_workspace_bytes(m, (ctypes.c_int64 * 1)(n), 1, k, 0)
+    assert need > (32 << 20), need
+    rc = _noalloc(lib)(VP(256), VP(256), VP(256), None, VP(256), 1, m, n, k,
+                                      VP(torch.cuda.current_stream().cuda_stream))
+    assert rc == 1 and b"maximum" in lib.pgs_last_error()
