@@ -47,17 +47,25 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+SHAPES = {"q": (HIDDEN, HIDDEN), "k": (KV, HIDDEN), "v": (KV, HIDDEN), "o": (HIDDEN, HIDDEN),
+          "gate": (INTER, HIDDEN), "up": (INTER, HIDDEN), "down": (HIDDEN, INTER)}
+
+
+def layer_weight(dev, l: int, j: int, n: int, k: int):
+    """fp32 weight j of layer l, ~N(0, 0.02) from its own seed (regenerated
+    bit for bit by the correctness gate)."""
+    g = torch.Generator(device=dev).manual_seed(1234 + 100 * l + j)
+    return torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02
+
+
 def make_layers(dev, layers: int):
     from pageserve_amd import quantization as Q
 
-    shapes = {"q": (HIDDEN, HIDDEN), "k": (KV, HIDDEN), "v": (KV, HIDDEN), "o": (HIDDEN, HIDDEN),
-              "gate": (INTER, HIDDEN), "up": (INTER, HIDDEN), "down": (HIDDEN, INTER)}
     out = []
     for l in range(layers):
         L = {}
-        for j, (name, (n, k)) in enumerate(shapes.items()):
-            g = torch.Generator(device=dev).manual_seed(1234 + 100 * l + j)
-            w = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02
+        for j, (name, (n, k)) in enumerate(SHAPES.items()):
+            w = layer_weight(dev, l, j, n, k)
             L[name] = Q.QuantizedWeight(w)
             del w
         for j, (name, n) in enumerate((("q_b", HIDDEN), ("k_b", KV), ("v_b", KV))):
@@ -389,6 +397,125 @@ def read_traffic(key):
     return None
 
 
+# ---------------------------------------------------------------------------
+# MFMA utilisation of the prefill launches from hardware counters: a
+# rocprofv3 --pmc pass (MfmaUtil, MfmaFlopsBF16, GRBM_GUI_ACTIVE) over
+# `--prefill-workload M`, which runs the four launch kinds of the prefill
+# sweep once per layer and records each kind's kernel instance
+# (pgs_last_plan) in a JSON file; `--mfma-summary` joins the two.
+# ---------------------------------------------------------------------------
+PREFILL_KINDS = ("q|k|v", "o", "gate|up", "down")
+
+
+def prefill_flops(m):
+    return {"q|k|v": 2 * m * (HIDDEN + 2 * KV) * HIDDEN, "o": 2 * m * HIDDEN * HIDDEN,
+            "gate|up": 4 * m * INTER * HIDDEN, "down": 2 * m * HIDDEN * INTER}
+
+
+def prefill_workload(dev, layers_n, m, plan_path):
+    from pageserve_amd import _native
+    from pageserve_amd import quantization as Q
+
+    layers = make_layers(dev, layers_n)
+    gen = torch.Generator(device=dev).manual_seed(31 + m)
+    x = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    xo = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    plans = {}
+    for L in layers:
+        Q.linear_group(x, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+        plans["q|k|v"] = _native.last_plan()
+        L["o"].linear(xo)
+        plans["o"] = _native.last_plan()
+        act = Q.swiglu(x, L["gate"], L["up"])
+        plans["gate|up"] = _native.last_plan()
+        L["down"].linear(act)
+        plans["down"] = _native.last_plan()
+    torch.cuda.synchronize()
+    with open(plan_path, "w") as f:
+        json.dump({"m": m, "layers": layers_n, "plans": plans, "flops": prefill_flops(m)}, f, indent=1)
+    log(f"[bench] prefill workload done: m={m}, {layers_n} layers x {len(PREFILL_KINDS)} launch kinds -> {plan_path}")
+
+
+def kernel_pattern(plan: str) -> tuple[str, str | None]:
+    """The demangled kernel name (template argument list) of a launch plan
+    string, and of its follow-up reduce kernel, if any."""
+    m = re.search(r"(launch_k64|launch_cfg|launch_instance)\(.*?\) \[(.*?)\]", plan)
+    if not m:
+        raise ValueError(f"unrecognised launch plan {plan!r}")
+    vals = [kv.split(" = ")[1] for kv in m.group(2).split(", ")]
+    name = {"launch_k64": "gemm_k64_kernel", "launch_cfg": "gemm_kernel", "launch_instance": "skinny_kernel"}[m.group(1)]
+    reduce = None
+    if "then gemm_reduce_kernel" in plan:
+        reduce = "gemm_reduce_kernel<" + ", ".join(vals[:4]) + ">"
+    return f"{name}<{', '.join(vals)}>", reduce
+
+
+def mfma_summary(pmc_dir, plan_path, command):
+    """Per launch kind: mean dispatch duration (the counter pass's own
+    timestamps), MfmaUtil, MFMA flops counted by the hardware, and the
+    algorithmic TFLOP/s against the 2.5 PFLOP/s bf16 dense peak."""
+    import csv
+    import glob
+    import statistics
+
+    with open(plan_path) as f:
+        plan = json.load(f)
+    rows = {}
+    for path in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                d = rows.setdefault((r["Kernel_Name"], r["Dispatch_Id"]), {"name": r["Kernel_Name"],
+                                                                          "id": r["Dispatch_Id"]})
+                d[r["Counter_Name"]] = float(r["Counter_Value"])
+                d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    m = plan["m"]
+    # the workload issues, per layer, the launch kinds in PREFILL_KINDS order
+    # (each followed by its reduce kernel when it has one): walk this
+    # package's dispatches in dispatch order and hand each to the next
+    # expected launch (q|k|v and o can be the same kernel instance)
+    seq = []
+    for kind in PREFILL_KINDS:
+        kname, reduce = kernel_pattern(plan["plans"][kind])
+        seq.append((kind, kname))
+        if reduce:
+            seq.append((kind + " (reduce)", reduce))
+    ours = sorted((d for d in rows.values() if any(pat in d["name"] for _, pat in seq)),
+                  key=lambda d: int(d["id"]))
+    by_kind = {kind: [] for kind, _ in seq}
+    i = 0
+    for d in ours:
+        for step in range(len(seq)):
+            kind, pat = seq[(i + step) % len(seq)]
+            if pat in d["name"]:
+                by_kind[kind].append(d)
+                i = (i + step + 1) % len(seq)
+                break
+    lines = [f"# MFMA utilisation of the prefill launches, M={m}, Qwen2.5-3B linears ({plan['layers']} layers)", "",
+             "Command (repository root):", "", "```", command, "```", "",
+             "Counters per dispatch from `rocprofv3 --pmc` (one pass: `MfmaUtil` = SQ_VALU_MFMA_BUSY_CYCLES summed "
+             "over SIMDs / (GRBM_GUI_ACTIVE x SIMDs), `MfmaFlopsBF16` = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512), "
+             "mean over the dispatches of each launch kind (assigned in dispatch order: the workload issues "
+             "q|k|v, o, gate|up, down per layer); durations from the same pass's dispatch timestamps "
+             "(kernels serialised by counter collection). Algorithmic flops = 2 M N K per linear (4 M N K for the "
+             "gate|up pair); the hardware count also includes the zero padding of partial tiles.", "",
+             "| launch | kernel | dispatches | mean us | MfmaUtil % | hw MFMA GFLOP | algorithmic GFLOP | "
+             "algorithmic TFLOP/s | % of 2.5 PFLOP/s |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for kind, pat in seq:
+        ds = by_kind[kind]
+        if not ds:
+            lines.append(f"| {kind} | `{pat}` | 0 | | | | | | |")
+            continue
+        us = statistics.mean(d["ns"] for d in ds) / 1e3
+        util = statistics.mean(d.get("MfmaUtil", float("nan")) for d in ds)
+        hw = statistics.mean(d.get("MfmaFlopsBF16", float("nan")) for d in ds) / 1e9
+        alg = plan["flops"][kind] / 1e9 if kind in plan["flops"] else 0.0
+        tf = alg * 1e9 / (us * 1e-6) / 1e12 if alg else 0.0
+        lines.append(f"| {kind} | `{pat}` | {len(ds)} | {us:.2f} | {util:.1f} | {hw:.2f} | {alg:.2f} | "
+                     f"{tf:.1f} | {100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f} |")
+    return "\n".join(lines) + "\n"
+
+
 def other_configs(layers, dev, steps):
     """The remaining workload sizes, one compact figure each: decode sweeps at
     M=4 and 16, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
@@ -437,8 +564,11 @@ def other_configs(layers, dev, steps):
         heads.append(Q.QuantizedWeight(w))
         del w
     torch.cuda.empty_cache()
+    gate_x, gate_logits = {}, {}
     for m in (1, 8, 256):
         x = act(m, HIDDEN)
+        gate_x[m] = x.float().cpu().numpy()
+        gate_logits[m] = heads[0].linear(x, out_dtype=torch.float32).cpu().numpy()
         g, _ = capture(lambda: [hw.linear(x, out_dtype=torch.float32) for hw in heads * 4])
         ms = time_graph(g, max(5, steps // 10), 2)
         per = ms * 1e3 / 8
@@ -446,7 +576,10 @@ def other_configs(layers, dev, steps):
         out[f"lm_head_m{m}"] = {"us_per_launch": round(per, 2), "GB/s": round(nbytes / (per * 1e-6) / 1e9, 1),
                                 "TFLOP/s": round(2 * m * vocab * HIDDEN / (per * 1e-6) / 1e12, 1)}
         del g
-    del heads
+    log("[bench] lm_head correctness gate (every row's argmax against the oracle)")
+    out["lm_head_correctness"] = lm_head_gate((heads[0].q.cpu().numpy(), heads[0].scale.cpu().numpy()), gate_x,
+                                              gate_logits)
+    del heads, gate_logits
     torch.cuda.empty_cache()
     # the single [4864, 896] linear at M=1 (Qwen2.5-0.5B gate_proj)
     w = torch.randn((4864, 896), generator=gen, device=dev) * 0.02
@@ -471,12 +604,14 @@ def other_configs(layers, dev, steps):
 
 
 def cpu_baseline(layers, m, budget_s):
+    """The reference's per-call path on this host's CPU cores over a sample
+    of layers: 3 warm-ups, the median of 10 timed passes."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference_cpu_path as R
 
     def get_layer(i):
         L = layers[i]
-        h = {name: (L[name].q.cpu(), L[name].scale.cpu()) for name in ("q", "k", "v", "o", "gate", "up", "down")}
+        h = {name: (L[name].q.cpu(), L[name].scale.cpu()) for name in SHAPES}
         for b in ("q_b", "k_b", "v_b"):
             h[b] = L[b].cpu()
         return h
@@ -484,6 +619,89 @@ def cpu_baseline(layers, m, budget_s):
     r = R.time_layers(get_layer, len(layers), m, budget_s=budget_s)
     info = R.cpu_model()
     return r, info
+
+
+def _sha(a) -> str:
+    import hashlib
+
+    return hashlib.sha256(a.tobytes()).hexdigest()[:16]
+
+
+def correctness_gate(dev, layers, inputs, check_layers):
+    """After the timed runs: the same launches as the timed sweeps, on the
+    same weights and inputs, against the oracle (oracle/quantization_oracle.py
+    on this host's CPU).  Per checked layer: every q and scale bit for bit
+    against the oracle quantizer run on the regenerated fp32 weights (their
+    sha256 prefixes recorded), and at each token count every launch kind of
+    the sweep -- q|k|v with bias, o, the fused gate|up, down on the kernel's
+    own gate|up output -- within the specification's tolerance (all rows at
+    up to 16 tokens, 16 sampled rows above)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import quantization_oracle as O
+    from pageserve_amd import quantization as Q
+
+    def np32(t):
+        return t.detach().float().cpu().numpy()
+
+    out = {"ok": True, "quantizer": [], "linears": []}
+    for l in check_layers:
+        L = layers[l]
+        ref_q = {}
+        for j, (name, (n, k)) in enumerate(SHAPES.items()):
+            qr, sr = O.quantize_per_channel(layer_weight(dev, l, j, n, k).cpu().numpy())
+            qg, sg = L[name].q.cpu().numpy(), L[name].scale.cpu().numpy()
+            ok = bool(np.array_equal(qg, qr) and np.array_equal(sg.view(np.uint32), sr.view(np.uint32)))
+            out["quantizer"].append({"layer": l, "weight": name, "bit_exact": ok, "q_sha256": _sha(qg),
+                                     "scale_sha256": _sha(sg)})
+            out["ok"] &= ok
+            ref_q[name] = (qr, sr)
+        for m, (x, xo) in inputs.items():
+            rows = np.arange(m) if m <= 16 else np.linspace(0, m - 1, 16).astype(int)
+            xn, xon = np32(x)[rows], np32(xo)[rows]
+            outs = Q.linear_group(x, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
+            act = Q.swiglu(x, L["gate"], L["up"])
+            got = {"q": outs[0], "k": outs[1], "v": outs[2], "o": L["o"].linear(xo), "gate|up": act,
+                   "down": L["down"].linear(act)}
+            actn = np32(act)[rows]
+            for name, y in got.items():
+                if name in ("q", "k", "v"):
+                    b = np32(L[name + "_b"])
+                    ref, acc, k = O.linear(xn, *ref_q[name], b), O.acc_bound(xn, *ref_q[name], b), HIDDEN
+                elif name == "o":
+                    ref, acc, k = O.linear(xon, *ref_q["o"]), O.acc_bound(xon, *ref_q["o"]), HIDDEN
+                elif name == "gate|up":
+                    qg_, qu_ = ref_q["gate"], ref_q["up"]
+                    ref, acc, k = O.swiglu(xn, *qg_, *qu_), O.swiglu_acc(xn, *qg_, *qu_), HIDDEN
+                else:
+                    ref, acc, k = O.linear(actn, *ref_q["down"]), O.acc_bound(actn, *ref_q["down"]), INTER
+                r = O.compare(np32(y)[rows], ref, k, bf16_out=True, acc=acc)
+                out["linears"].append({"layer": l, "m": m, "launch": name, "ok": r["ok"], "rel": round(r["rel"], 6),
+                                       "worst_vs_bound": round(r["worst_vs_bound"], 4), "rows": len(rows)})
+                out["ok"] &= r["ok"]
+    return out
+
+
+def lm_head_gate(heads_q, x_by_m, logits_by_m):
+    """int8 lm_head: fp32 logits of every row within the tolerance and the
+    argmax of every row equal to the oracle's (blocked float64 oracle)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import quantization_oracle as O
+
+    q, s = heads_q
+    res = {"ok": True}
+    for m, x in x_by_m.items():
+        ref = np.concatenate([O.linear(x, q[i:i + 16384], s[i:i + 16384]) for i in range(0, q.shape[0], 16384)], axis=1)
+        got = logits_by_m[m]
+        r = O.compare(got, ref, HIDDEN)
+        am = bool(np.array_equal(O.argmax_rows(got), O.argmax_rows(ref)))
+        res[f"m{m}"] = {"rows": m, "argmax_equal_every_row": am, "rel": r["rel"], "ok": r["ok"] and am,
+                        "min_top2_gap": float(O.top2_gap(ref).min())}
+        res["ok"] &= r["ok"] and am
+    return res
 
 
 def main():
@@ -495,7 +713,10 @@ def main():
     ap.add_argument("--prefill-m", type=int, default=512)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for the baseline")
+    ap.add_argument("--cpu-prefill-budget", type=float, default=8.0,
+                    help="seconds of CPU work for the prefill baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gate", action="store_true", help="skip the correctness gate (profiling runs)")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "configs"], default="all")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workload sizes")
     ap.add_argument("--no-torch-ref", action="store_true",
@@ -504,9 +725,24 @@ def main():
                     help="run only the dispatches the rocprofv3 --pmc traffic passes read")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="reduce rocprofv3 --pmc output directories to the traffic summary (no GPU)")
+    ap.add_argument("--prefill-workload", type=int, metavar="M",
+                    help="run only the prefill sweep's launches once per layer at M tokens (counter passes)")
+    ap.add_argument("--plan-file", default="gpurun_out/prefill_plans.json",
+                    help="where --prefill-workload records each launch kind's kernel instance")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "PLAN_FILE"),
+                    help="reduce a rocprofv3 --pmc pass over --prefill-workload to an MFMA table (no GPU)")
+    ap.add_argument("--summary-out", help="file --mfma-summary writes (stdout too)")
     ap.add_argument("--pmc-command", action="append", default=[],
                     help="command line recorded in the traffic summary (repeatable)")
     args = ap.parse_args()
+
+    if args.mfma_summary:
+        text = mfma_summary(args.mfma_summary[0], args.mfma_summary[1], " ".join(args.pmc_command))
+        if args.summary_out:
+            with open(args.summary_out, "w") as f:
+                f.write(text)
+        print(text, end="")
+        return
 
     if args.pmc_summary:
         text = pmc_summary(args.pmc_summary, args.pmc_command)
@@ -534,11 +770,17 @@ def main():
         with torch.inference_mode():
             pmc_workload(dev, args.layers)
         return
+    if args.prefill_workload:
+        os.makedirs(os.path.dirname(os.path.abspath(args.plan_file)), exist_ok=True)
+        with torch.inference_mode():
+            prefill_workload(dev, args.layers, args.prefill_workload, args.plan_file)
+        return
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; building {args.layers} layers of int8 weights")
     layers = make_layers(dev, args.layers)
     gen = torch.Generator(device=dev).manual_seed(99 + args.m)
 
     result = {}
+    gate_inputs = {}
     with torch.inference_mode():
         # ---------------- decode, M = m ----------------
         m = args.m
@@ -546,6 +788,7 @@ def main():
         xo = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
         xi = torch.randn((m, INTER), generator=gen, device=dev).to(torch.bfloat16)
         if args.only in ("all", "decode"):
+            gate_inputs[m] = (x, xo)
             step, nbytes, nflops, launches = fused_sweep(layers, x, xo, m)
             eager_out = step()
             g, graph_out = capture(step)
@@ -618,6 +861,7 @@ def main():
             pm = args.prefill_m
             px = torch.randn((pm, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
             pxo = torch.randn((pm, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+            gate_inputs[pm] = (px, pxo)
             step, nbytes, nflops, launches = fused_sweep(layers, px, pxo, pm)
             g, _ = capture(step)
             psteps = max(10, args.steps // 4)
@@ -650,19 +894,43 @@ def main():
                 log(f"[bench] {key}: {v}")
             result["other_configs"] = oc
 
+        # ---------------- correctness gate (after all timing) ----------------
+        if gate_inputs and not args.no_gate:
+            log("[bench] correctness gate: quantizer bits and every launch kind of the sweeps against the oracle")
+            t0 = time.perf_counter()
+            gate = correctness_gate(dev, layers, gate_inputs, sorted({0, len(layers) - 1}))
+            gate["seconds"] = round(time.perf_counter() - t0, 1)
+            result["correctness"] = gate
+            log(f"[bench] correctness gate: ok={gate['ok']} ({gate['seconds']} s)")
+
         # ---------------- CPU baseline ----------------
         if not args.no_cpu_baseline and args.only in ("all", "decode"):
             r, info = cpu_baseline(layers, args.m, args.cpu_budget)
             gbs = r["bytes"] / r["seconds"] / 1e9
-            log(f"[bench] CPU baseline: {r['layers']} layers in {r['seconds']:.2f} s on {r['threads']} threads "
-                f"({info['model']}): {gbs:.3f} GB/s")
+            log(f"[bench] CPU baseline: {r['layers']} layers per pass, median {r['seconds']:.3f} s on "
+                f"{r['threads']} threads ({info['model']}): {gbs:.3f} GB/s")
             result["cpu_baseline"] = {
                 "value": round(gbs, 4), "unit": "GB/s", "cores": r["threads"], "kind": "port",
                 "sample": (f"layers 0..{r['layers'] - 1} of the {args.layers}-layer M={args.m} sweep, 7 per-call "
-                           f"linears each: (q.float()*scale).to(bf16) then F.linear, torch CPU, "
-                           f"{r['seconds']:.2f} s"),
+                           f"linears each: (q.float()*scale).to(bf16) then F.linear, torch CPU; {r['warmup']} "
+                           f"warm-up passes, median of {len(r['runs'])} timed passes ({r['seconds']:.3f} s each)"),
                 "cpu": info["model"], "amx_bf16": info["amx_bf16"], "avx512f": info["avx512f"],
+                "runs_s": [round(v, 4) for v in r["runs"]],
             }
+            if args.prefill_m > 0 and args.only == "all":
+                pr, _ = cpu_baseline(layers, args.prefill_m, args.cpu_prefill_budget)
+                tf = pr["flops"] / pr["seconds"] / 1e12
+                log(f"[bench] CPU baseline, prefill M={args.prefill_m}: {pr['layers']} layer per pass, median "
+                    f"{pr['seconds']:.3f} s: {tf:.3f} TFLOP/s")
+                result["cpu_baseline"]["prefill"] = {
+                    "value": round(tf, 4), "unit": "TFLOP/s", "cores": pr["threads"], "kind": "port",
+                    "ms_per_step_scaled": round(pr["seconds"] * 1e3 * args.layers / pr["layers"], 1),
+                    "sample": (f"layers 0..{pr['layers'] - 1} at M={args.prefill_m}, the same 7 per-call linears; "
+                               f"{pr['warmup']} warm-ups, median of {len(pr['runs'])} passes "
+                               f"({pr['seconds']:.3f} s each); ms_per_step_scaled = that median x "
+                               f"{args.layers}/{pr['layers']} layers"),
+                    "runs_s": [round(v, 4) for v in pr["runs"]],
+                }
 
     line = {
         "metric": "W8A16 linear GB/s (% HBM peak) at M=1; TFLOPS (% MFMA peak) at M=512",
@@ -676,7 +944,8 @@ def main():
                    "weight_dtype": "int8", "activation_dtype": "bf16", "accumulate": "fp32",
                    "parallelism": "none (1 GPU)"},
     }
-    for key in ("roofline", "cpu_baseline", "prefill", "per_call_sweep", "torch_gpu", "decode_detail", "other_configs"):
+    for key in ("roofline", "cpu_baseline", "correctness", "prefill", "per_call_sweep", "torch_gpu", "decode_detail",
+                "other_configs"):
         if key in result:
             line[key] = result[key]
     print(json.dumps(line), flush=True)

@@ -13,6 +13,7 @@ torch calls on CPU tensors.
 from __future__ import annotations
 
 import os
+import statistics
 import time
 
 import torch
@@ -51,22 +52,8 @@ def cpu_model() -> dict:
     return info
 
 
-def time_layers(get_layer, n_layers: int, m: int, budget_s: float = 12.0, seed: int = 99) -> dict:
-    """Times the 7 per-call linears of as many layers as fit in ``budget_s``.
-
-    ``get_layer(i)`` returns layer i as CPU tensors {name: (q int8 [N,K],
-    scale fp32 [N,1])} plus optional "q_b"/"k_b"/"v_b" bf16 biases (fetched
-    before its timing starts).  Returns seconds, layers timed and the
-    algorithmic bytes / flops of the timed calls.
-    """
-    torch.set_num_threads(cpu_threads())
-    g = torch.Generator().manual_seed(seed)
-    first = get_layer(0)
-    hidden = first["q"][0].shape[1]
-    inter = first["gate"][0].shape[0]
-    x = torch.randn(m, hidden, generator=g).to(torch.bfloat16)
-    xi = torch.randn(m, inter, generator=g).to(torch.bfloat16)
-    order = ("q", "k", "v", "o", "gate", "up", "down")
+def _layer_runner(x, xi, order=("q", "k", "v", "o", "gate", "up", "down")):
+    m = x.shape[0]
 
     def run_layer(L):
         nbytes = flops = 0
@@ -80,20 +67,43 @@ def time_layers(get_layer, n_layers: int, m: int, budget_s: float = 12.0, seed: 
             flops += 2 * m * n * k
         return nbytes, flops
 
+    return run_layer
+
+
+def time_layers(get_layer, n_layers: int, m: int, budget_s: float = 12.0, seed: int = 99, warmup: int = 3,
+                runs: int = 10) -> dict:
+    """Times the reference's 7 per-call linears over a sample of layers:
+    ``warmup`` untimed passes, then the median of ``runs`` timed passes over
+    the first ``count`` layers, ``count`` chosen so that all passes fit about
+    ``budget_s`` seconds.
+
+    ``get_layer(i)`` returns layer i as CPU tensors {name: (q int8 [N,K],
+    scale fp32 [N,1])} plus optional "q_b"/"k_b"/"v_b" bf16 biases (all
+    sampled layers are fetched before any timing).  Returns the median pass's
+    seconds, the layers per pass, the algorithmic bytes / flops of one pass,
+    every pass's seconds and the thread count.
+    """
+    torch.set_num_threads(cpu_threads())
+    g = torch.Generator().manual_seed(seed)
+    first = get_layer(0)
+    hidden = first["q"][0].shape[1]
+    inter = first["gate"][0].shape[0]
+    x = torch.randn(m, hidden, generator=g).to(torch.bfloat16)
+    xi = torch.randn(m, inter, generator=g).to(torch.bfloat16)
+    run_layer = _layer_runner(x, xi)
     with torch.inference_mode():
-        for _ in range(3):  # warm-up (thread pools, allocator)
-            run_layer(first)
+        run_layer(first)  # thread pools, allocator
         t0 = time.perf_counter()
         run_layer(first)
         per_layer = time.perf_counter() - t0
-        count = max(1, min(n_layers, int(budget_s / max(per_layer, 1e-6))))
-        total_b = total_f = 0
-        secs = 0.0
-        for i in range(count):
-            L = first if i == 0 else get_layer(i)
+        count = max(1, min(n_layers, int(budget_s / max(per_layer, 1e-6) / (warmup + runs))))
+        layers = [first] + [get_layer(i) for i in range(1, count)]
+        secs = []
+        for rep in range(warmup + runs):
             t0 = time.perf_counter()
-            b, f = run_layer(L)
-            secs += time.perf_counter() - t0
-            total_b += b
-            total_f += f
-    return {"seconds": secs, "layers": count, "bytes": total_b, "flops": total_f, "threads": cpu_threads()}
+            totals = [run_layer(L) for L in layers]
+            if rep >= warmup:
+                secs.append(time.perf_counter() - t0)
+    med = statistics.median(secs)
+    return {"seconds": med, "layers": count, "bytes": sum(b for b, _ in totals), "flops": sum(f for _, f in totals),
+            "threads": cpu_threads(), "runs": secs, "warmup": warmup}
