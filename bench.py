@@ -123,6 +123,36 @@ def per_call_sweep(layers, x, xo, xi, m):
     return step, per_layer_b * len(layers), per_layer_f * len(layers), 7 * len(layers)
 
 
+def dropin_sweep(layers, x, xo, xi):
+    """The reference's own call structure through the drop-in (engine/model.py
+    :25-26, 168-190): ``F.linear(h, _resolve(W), b)`` with ``_resolve(W) =
+    W.get()`` on bf16-model QuantizedWeights (the same int8 storage), the
+    SwiGLU as ``F.silu(gate) * up`` in torch; 7 linears per layer."""
+    import torch.nn.functional as F
+
+    from pageserve_amd import quantization as Q
+
+    def bf16_view(w):
+        st = dict(w.state())
+        st["meta"] = torch.tensor([w.shape[0], w.shape[1], 1], dtype=torch.int64)
+        return Q.QuantizedWeight.from_state(st)
+
+    views = [{name: bf16_view(L[name]) for name in SHAPES} for L in layers]
+
+    def step():
+        y = None
+        for L, W in zip(layers, views):
+            F.linear(x, W["q"].get(), L["q_b"])
+            F.linear(x, W["k"].get(), L["k_b"])
+            F.linear(x, W["v"].get(), L["v_b"])
+            F.linear(xo, W["o"].get())
+            act = F.silu(F.linear(x, W["gate"].get())) * F.linear(x, W["up"].get())
+            y = F.linear(act, W["down"].get())
+        return y
+
+    return step
+
+
 def torch_gpu_entry(ref_ms, dense_ms, ours_ms, work, unit):
     """Report line for the torch comparison: the same work per sweep (this
     package's algorithmic bytes or flops) over each path's time."""
@@ -806,7 +836,11 @@ def main():
             pg, _ = capture(pstep)
             pms = time_graph(pg, args.steps, args.warmup)
             pval = pbytes / (pms * 1e-3) / 1e9
-            log(f"[bench] per-call sweep (7 launches/layer): {pms * 1e3:.1f} us, {pval:.1f} GB/s")
+            pms_eager = time_eager(pstep, max(5, args.steps // 10), 3)
+            dstep = dropin_sweep(layers, x, xo, xi)
+            dms_eager = time_eager(dstep, max(5, args.steps // 10), 3)
+            log(f"[bench] per-call sweep (7 launches/layer): {pms * 1e3:.1f} us graph, {pms_eager * 1e3:.1f} us eager; "
+                f"through F.linear(x, W.get(), b) eagerly: {dms_eager * 1e3:.1f} us")
             del g, pg
             ref_ms = dense_ms = None
             if not args.no_torch_ref:
@@ -851,7 +885,11 @@ def main():
                                       "reference_structure_us_per_layer": round(chain["reference"], 3)}},
                 "per_call_sweep": {"ms_per_step": round(pms, 5), "gbs": round(pval, 2),
                                    "frac_of_hbm_peak": round(pval / HBM_PEAK_GBS, 4),
-                                   "bytes_per_step": pbytes, "launches_per_step": plaunch},
+                                   "bytes_per_step": pbytes, "launches_per_step": plaunch,
+                                   "eager_ms_per_step": round(pms_eager, 5),
+                                   "dropin_f_linear_eager_ms_per_step": round(dms_eager, 5),
+                                   "dropin_what": "engine/model.py's own calls, F.linear(h, W.get(), b) on bf16-model "
+                                                  "QuantizedWeights and F.silu(gate) * up in torch, launched eagerly"},
             })
             if ref_ms is not None:
                 result["torch_gpu"] = torch_gpu_entry(ref_ms, dense_ms, ms, nbytes, "GB/s")

@@ -109,7 +109,9 @@ def load(path: Path | None = None) -> ctypes.CDLL:
                 "`python -m pageserve_amd.build` (there is no fallback implementation)"
             )
         try:
-            lib = ctypes.CDLL(str(p))
+            # global: the C++ host module (_pgs_host) links against this
+            # library and binds to the copy loaded here
+            lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
         except OSError as e:
             raise NativeLibraryError(f"pageserve_amd: cannot load {p}: {e}") from e
         for name, (res, args) in SIGNATURES.items():
@@ -122,6 +124,38 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+_host = None
+
+
+def load_host():
+    """The C++ host module (``_lib/_pgs_host*.so``, built by
+    ``pageserve_amd.build``): the argument checks, output allocation and
+    C-ABI call of the linear entry points without Python per-call overhead.
+    Loaded once, after the library it calls."""
+    global _host
+    if _host is not None:
+        return _host
+    load()
+    import importlib.machinery
+    import importlib.util
+
+    cands = sorted(LIB_PATH.parent.glob("_pgs_host*.so"))
+    if not cands:
+        raise NativeLibraryError(f"pageserve_amd: C++ host module not found in {LIB_PATH.parent}; build it with "
+                                 "`python -m pageserve_amd.build`")
+    loader = importlib.machinery.ExtensionFileLoader("_pgs_host", str(cands[0]))
+    spec = importlib.util.spec_from_file_location("_pgs_host", str(cands[0]), loader=loader)
+    try:
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+    except ImportError as e:
+        raise NativeLibraryError(f"pageserve_amd: cannot load the C++ host module {cands[0]}: {e}") from e
+    if mod.abi_version() != ABI_VERSION:
+        raise NativeLibraryError(f"pageserve_amd: host module bound to ABI {mod.abi_version()} != {ABI_VERSION}")
+    _host = mod
+    return mod
 
 
 def last_plan() -> str:

@@ -28,6 +28,9 @@ INCLUDE = ROOT / "include"
 LIBDIR = PKG / "_lib"
 LIBNAME = "libpageserve_amd.so"
 OBJDIR = ROOT / "_build" / "obj"
+HOST_SRC = CSRC / "host_ops.cpp"
+HOST_NAME = "_pgs_host"
+HOST_BUILD = ROOT / "_build" / "host"
 
 ARCH = "gfx950"
 
@@ -109,14 +112,51 @@ def build(verbose: bool = True) -> Path:
     LIBDIR.mkdir(parents=True, exist_ok=True)
     out = LIBDIR / LIBNAME
     tmp = LIBDIR / (LIBNAME + ".tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # the soname lets the host module's dependency on this library resolve
+    # to the copy already loaded from the package directory
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIBNAME}", *map(str, objs), "-o",
+           str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, out)
     if verbose:
         print(f"[pageserve_amd.build] built {out} from {len(srcs)} sources for {ARCH}")
+    build_host(verbose)
     return out
+
+
+def build_host(verbose: bool = True) -> Path:
+    """Compiles the C++ host module (host_ops.cpp, a PyTorch extension that
+    calls the C ABI) into ``_lib/_pgs_host*.so``.  Always rebuilds."""
+    import ctypes
+
+    import torch.utils.cpp_extension as ext
+
+    # the module's dependency on the library resolves by soname to a copy
+    # already loaded (load() imports the module right after linking it)
+    ctypes.CDLL(str(LIBDIR / LIBNAME), mode=ctypes.RTLD_GLOBAL)
+    shutil.rmtree(HOST_BUILD, ignore_errors=True)
+    HOST_BUILD.mkdir(parents=True, exist_ok=True)
+    ext.load(
+        name=HOST_NAME,
+        sources=[str(HOST_SRC)],
+        build_directory=str(HOST_BUILD),
+        extra_include_paths=[str(INCLUDE), "/opt/rocm/include"],
+        # torch's HIP headers need the platform macro outside hipcc
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__"],
+        extra_ldflags=[f"-L{LIBDIR}", "-lpageserve_amd"],
+        with_cuda=False,
+        verbose=False,
+    )
+    built = next(HOST_BUILD.glob(f"{HOST_NAME}*.so"))
+    dst = LIBDIR / built.name
+    tmp = LIBDIR / (built.name + ".tmp")
+    shutil.copyfile(built, tmp)
+    os.replace(tmp, dst)
+    if verbose:
+        print(f"[pageserve_amd.build] built {dst} (C++ host module)")
+    return dst
 
 
 if __name__ == "__main__":

@@ -38,7 +38,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _native
-from ._native import DTYPE_BF16, DTYPE_F16, DTYPE_F32, LinearOut, check
+from ._native import DTYPE_BF16, DTYPE_F16, DTYPE_F32, check
 
 __all__ = [
     "quantize_per_channel",
@@ -316,24 +316,16 @@ def _dequantize_packed(qp: torch.Tensor, scale: torch.Tensor, n: int, k: int, dt
 # fused linears
 # ---------------------------------------------------------------------------
 
-def _check_x(x: torch.Tensor, k: int, device: torch.device, what: str) -> torch.Tensor:
-    if not isinstance(x, torch.Tensor):
-        raise TypeError(f"{what}: input must be a torch.Tensor")
-    if x.device != device:
-        raise ValueError(f"{what}: input on {x.device} but weight on {device}")
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"{what}: the W8A16 kernels take bf16 activations, got {x.dtype}")
-    if x.shape[-1] != k:
-        raise ValueError(f"{what}: input has {x.shape[-1]} features, weight expects {k}")
-    return _aligned(x.reshape(-1, k))
-
-
-def _check_bias(bias: torch.Tensor | None, n: int, device: torch.device, what: str) -> torch.Tensor | None:
-    if bias is None:
-        return None
-    if bias.device != device or bias.dtype != torch.bfloat16 or bias.numel() != n:
-        raise ValueError(f"{what}: bias must be a bf16 [{n}] tensor on {device}")
-    return _aligned(bias.reshape(n), 2)
+def _ws_args(dev: torch.device, x, k: int, ns: tuple, swiglu: bool, norm: bool) -> tuple[int, int]:
+    """(pointer, bytes) of the K-split workspace a call needs, (0, 0) when its
+    plan splits nothing (every decode projection of a 2048-hidden model)."""
+    m = x.numel() // k if isinstance(x, torch.Tensor) and k else 0
+    if m <= 0 or _ws_need(m, ns, k, swiglu, norm) == 0:
+        return 0, 0
+    lib = _native.load()
+    with _on_device(dev):
+        ws, nbytes = _workspace(lib, dev, _raw_stream(dev), m, ns, k, swiglu, norm)
+    return ws.value or 0, nbytes
 
 
 def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
@@ -349,41 +341,14 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
     out: optional contiguous result buffer of the right shape and dtype; it
     may be the residual itself (in place).
     """
-    if residual is None and out is None:
-        return linear_group(x, [weight], [bias], out_dtype=out_dtype)[0]
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
-    dev = weight.device
-    if dev.type != "cuda":
+    if weight.device.type != "cuda":
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
-    n, k = weight.shape
-    lead = x.shape[:-1]
-    x2 = _check_x(x, k, dev, "linear")
-    m = x2.shape[0]
-    bb = _check_bias(bias, n, dev, "linear")
-    res = None
-    if residual is not None:
-        if residual.device != dev or residual.dtype != torch.bfloat16 or residual.shape[-1] != n \
-                or residual.numel() != m * n:
-            raise ValueError(f"linear: residual must be a bf16 [..., {n}] tensor with {m} rows on {dev}")
-        res = residual.reshape(m, n)
-        if not res.is_contiguous():
-            res = res.contiguous()
-    if out is None:
-        y = torch.empty((m, n), dtype=out_dtype, device=dev)
-    else:
-        if out.device != dev or out.dtype != out_dtype or out.numel() != m * n or not out.is_contiguous():
-            raise ValueError(f"linear: out must be a contiguous {out_dtype} tensor of {m * n} elements on {dev}")
-        y = out.view(m, n)
-    q, s = weight._kernel_operands()
-    lib = _native.load()
-    with _on_device(dev):
-        stream = _raw_stream(dev)
-        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, False)
-        rc = lib.pgs_w8a16_linear_residual(_ptr(x2), _ptr(q), _ptr(s), _ptr(bb), _ptr(res), _ptr(y),
-                                           _DTYPE_CODE[out_dtype], m, n, k, ws, ws_bytes, ctypes.c_void_p(stream))
-    check(rc, "w8a16 linear")
-    return y.reshape(*lead, n)
+    q, s, n, k, dev = weight._launch_operands()
+    ws, ws_bytes = _ws_args(dev, x, k, (n,), False, False)
+    return _native.load_host().linear(x, [q], [s], [bias], [n], k, out_dtype is torch.float32, residual, out, None,
+                                      0.0, ws, ws_bytes)[0]
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -487,13 +452,6 @@ def rmsnorm_linear_group(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return _linear_group(x, weights, biases, out_dtype, norm_weight, eps)
 
 
-def _norm_weight(w: torch.Tensor, k: int, dev: torch.device, what: str) -> torch.Tensor:
-    if not isinstance(w, torch.Tensor) or w.dtype != torch.bfloat16 or w.numel() != k or w.device != dev:
-        raise ValueError(f"{what}: norm weight must be a bf16 [{k}] tensor on {dev}")
-    w = w.reshape(k)
-    return w if w.is_contiguous() and w.data_ptr() % 16 == 0 else _aligned(w)
-
-
 def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch.Tensor]:
     if not weights or len(weights) > _native.MAX_GROUP:
         raise ValueError(f"linear_group takes 1..{_native.MAX_GROUP} weights")
@@ -502,45 +460,17 @@ def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch
         raise ValueError("one bias (or None) per weight")
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
-    w0 = weights[0]
-    dev = w0.device
-    if dev.type != "cuda":
+    if weights[0].device.type != "cuda":
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
-    k = w0.shape[1]
-    for w in weights:
-        if w.device != dev or w.shape[1] != k:
+    ops = [w._launch_operands() for w in weights]
+    _, _, _, k, dev = ops[0]
+    for o in ops:
+        if o[3] != k or o[4] != dev:
             raise ValueError("linear_group: weights must share device and in_features")
-    lead = x.shape[:-1]
-    x2 = _check_x(x, k, dev, "linear")
-    m = x2.shape[0]
-    nw = _norm_weight(norm_weight, k, dev, "rmsnorm_linear_group") if norm_weight is not None else None
-    lib = _native.load()
-    outs = (LinearOut * len(weights))()
-    ys, keep = [], []
-    for i, (w, b) in enumerate(zip(weights, biases)):
-        n = w.shape[0]
-        bb = _check_bias(b, n, dev, "linear")
-        y = torch.empty((m, n), dtype=out_dtype, device=dev)
-        q, s = w._kernel_operands()
-        keep.extend([q, s, bb])
-        outs[i].qp = q.data_ptr() if q.numel() else None
-        outs[i].scale = s.data_ptr() if s.numel() else None
-        outs[i].bias = bb.data_ptr() if bb is not None else None
-        outs[i].y = y.data_ptr() if y.numel() else None
-        outs[i].n = n
-        ys.append(y)
-    with _on_device(dev):
-        stream = _raw_stream(dev)
-        ws, ws_bytes = _workspace(lib, dev, stream, m, tuple(w.shape[0] for w in weights), k, False, nw is not None)
-        if nw is None:
-            rc = lib.pgs_w8a16_linear_group(_ptr(x2), outs, len(weights), _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
-                                            ctypes.c_void_p(stream))
-        else:
-            rc = lib.pgs_w8a16_rmsnorm_linear_group(_ptr(x2), _ptr(nw), ctypes.c_float(eps), outs, len(weights),
-                                                    _DTYPE_CODE[out_dtype], m, k, ws, ws_bytes,
-                                                    ctypes.c_void_p(stream))
-    check(rc, "w8a16 linear")
-    return [y.reshape(*lead, y.shape[1]) for y in ys]
+    qs, ss, ns = [o[0] for o in ops], [o[1] for o in ops], tuple(o[2] for o in ops)
+    ws, ws_bytes = _ws_args(dev, x, k, ns, False, norm_weight is not None)
+    return _native.load_host().linear(x, qs, ss, biases, ns, k, out_dtype is torch.float32, None, None, norm_weight,
+                                      eps, ws, ws_bytes)
 
 
 def swiglu(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight") -> torch.Tensor:
@@ -563,26 +493,10 @@ def _swiglu(x, gate, up, norm_weight, eps) -> torch.Tensor:
         raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
     if gate.shape != up.shape:
         raise ValueError("swiglu: gate and up weights must have the same shape")
-    n, k = gate.shape
-    lead = x.shape[:-1]
-    x2 = _check_x(x, k, dev, "swiglu")
-    m = x2.shape[0]
-    act = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    qg, sg = gate._kernel_operands()
-    qu, su = up._kernel_operands()
-    nw = _norm_weight(norm_weight, k, dev, "rmsnorm_swiglu") if norm_weight is not None else None
-    lib = _native.load()
-    with _on_device(dev):
-        stream = _raw_stream(dev)
-        ws, ws_bytes = _workspace(lib, dev, stream, m, (n,), k, True, nw is not None)
-        if nw is None:
-            rc = lib.pgs_w8a16_swiglu(_ptr(x2), _ptr(qg), _ptr(sg), _ptr(qu), _ptr(su), _ptr(act), m, n, k, ws,
-                                      ws_bytes, ctypes.c_void_p(stream))
-        else:
-            rc = lib.pgs_w8a16_rmsnorm_swiglu(_ptr(x2), _ptr(nw), ctypes.c_float(eps), _ptr(qg), _ptr(sg), _ptr(qu),
-                                              _ptr(su), _ptr(act), m, n, k, ws, ws_bytes, ctypes.c_void_p(stream))
-    check(rc, "w8a16 swiglu")
-    return act.reshape(*lead, n)
+    qg, sg, n, k, _ = gate._launch_operands()
+    qu, su, _, _, _ = up._launch_operands()
+    ws, ws_bytes = _ws_args(dev, x, k, (n,), True, norm_weight is not None)
+    return _native.load_host().swiglu(x, qg, sg, qu, su, n, k, norm_weight, eps, ws, ws_bytes)
 
 
 def mlp(x: torch.Tensor, gate: "QuantizedWeight", up: "QuantizedWeight", down: "QuantizedWeight",
@@ -644,7 +558,14 @@ class QuantizedWeight:
 
     def get(self) -> torch.Tensor:
         if self.qp.device.type == "cuda":
-            return W8A16Weight(self)
+            # one view per (qp, scale) storage: engine/model.py's _resolve calls
+            # get() before every projection, and building the tensor subclass
+            # costs about a microsecond of host time
+            v = getattr(self, "_view", None)
+            if v is None or v[0] is not self.qp or v[1] is not self.scale:
+                v = (self.qp, self.scale, W8A16Weight(self))
+                self._view = v
+            return v[2]
         return self.dense()
 
     def to(self, device) -> "QuantizedWeight":
@@ -715,6 +636,19 @@ class QuantizedWeight:
         if qp is qp0 and (not s.numel() or s.data_ptr() == sc0.data_ptr()):
             self._ops = (qp0, sc0, qp, s)
         return qp, s
+
+    def _launch_operands(self) -> tuple:
+        """(packed q, fp32 scale [N], N, K, device) for a launch, cached for
+        the current (qp, scale) objects (the per-call host path)."""
+        c = getattr(self, "_launch", None)
+        if c is not None and c[0] is self.qp and c[1] is self.scale:
+            return c[2]
+        q, s = self._kernel_operands()
+        ops = (q, s, self.shape[0], self.shape[1], q.device)
+        cached = getattr(self, "_ops", None)  # set when q and s are the stored tensors themselves
+        if cached is not None and cached[0] is self.qp and cached[1] is self.scale:
+            self._launch = (self.qp, self.scale, ops)
+        return ops
 
 
 def packed_numel(n: int, k: int) -> int:

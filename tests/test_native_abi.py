@@ -182,3 +182,11 @@ def test_capture_state_arguments(native_lib):
         assert (cap.value, cid.value) == (0, 0)  # the null stream is not capturing
     else:
         assert rc == 4 and not _has_gpu()
+
+
+def test_host_module_loads_and_matches_the_abi(native_lib):
+    """The C++ host module (the eager fast path of linear / linear_group /
+    swiglu) loads on a machine without a GPU and is bound to this ABI."""
+    host = _native.load_host()
+    assert host.abi_version() == _native.ABI_VERSION
+    assert callable(host.linear) and callable(host.swiglu)
