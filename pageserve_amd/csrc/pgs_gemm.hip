@@ -26,8 +26,6 @@
 //  * Workgroup ids are remapped so the units sharing a weight panel (same
 //    weight rows and K split) run on the same XCD (dispatch is round robin
 //    over the 8 XCDs, each with its own L2).
-#include <stdio.h>
-#include <stdlib.h>
 #include <type_traits>
 #include <utility>
 
@@ -761,17 +759,6 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
     const int min_steps = p.tiles < 128 ? 8 : 32;
     while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 1024 && kb / (p.splits * 2) >= min_steps)
       p.splits *= 2;
-  }
-  // EXPERIMENT-OVERRIDE (temporary)
-  if (const char* ov = getenv("PGS_GEMM_PLAN")) {
-    int bm = 0, sp = 0;
-    if (nmat == 1 && m > 128 && k % kBK == 0 && sscanf(ov, "%d,%d", &bm, &sp) == 2) {
-      p.bm = bm; p.bn = kBN; p.kg = 1;
-      p.tiles_m = (m + bm - 1) / bm;
-      int tn = 0;
-      for (int i = 0; i < members; ++i) tn += (n[i] + kBN - 1) / kBN;
-      p.tiles_n = tn; p.tiles = p.tiles_m * tn; p.splits = can_split ? sp : 1;
-    }
   }
   return p;
 }
