@@ -337,12 +337,12 @@ COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
 # summary key -> pattern on the demangled kernel name: the number-of-matrices
 # template argument is 2 for the gate|up pair (skinny_kernel<NW, U, NB, NMAT,
-# ...>, gemm_k64_kernel<BM, BN, NMAT, ...>; the profiler's demangler may drop
+# ...>, gemm_dma_kernel<BM, BN, NMAT, ...>; the profiler's demangler may drop
 # the first template argument, hence the optional group)
 PMC_KERNELS = {
     "copy": r"neg_kernel",
     "skinny_gate_up_m1": r"skinny_kernel<(\d+, )?\d+, \d+, 2, false",
-    "gemm_gate_up_m512": r"gemm_k64_kernel<(\d+, )?\d+, 2, false|gemm_kernel<(\d+, )?\d+, 2, false",
+    "gemm_gate_up_m512": r"gemm_(dma|k64)_kernel<(\d+, )?\d+, 2, false|gemm_kernel<(\d+, )?\d+, 2, false",
 }
 
 
@@ -469,11 +469,12 @@ def prefill_workload(dev, layers_n, m, plan_path):
 def kernel_pattern(plan: str) -> tuple[str, str | None]:
     """The demangled kernel name (template argument list) of a launch plan
     string, and of its follow-up reduce kernel, if any."""
-    m = re.search(r"(launch_k64|launch_cfg|launch_instance)\(.*?\) \[(.*?)\]", plan)
+    m = re.search(r"(launch_k64|launch_dma|launch_cfg|launch_instance)\(.*?\) \[(.*?)\]", plan)
     if not m:
         raise ValueError(f"unrecognised launch plan {plan!r}")
     vals = [kv.split(" = ")[1] for kv in m.group(2).split(", ")]
-    name = {"launch_k64": "gemm_k64_kernel", "launch_cfg": "gemm_kernel", "launch_instance": "skinny_kernel"}[m.group(1)]
+    name = {"launch_k64": "gemm_k64_kernel", "launch_dma": "gemm_dma_kernel", "launch_cfg": "gemm_kernel",
+            "launch_instance": "skinny_kernel"}[m.group(1)]
     reduce = None
     if "then gemm_reduce_kernel" in plan:
         reduce = "gemm_reduce_kernel<" + ", ".join(vals[:4]) + ">"
@@ -916,7 +917,7 @@ def main():
             proof = kernel_roofline(layers, lambda L: Q.swiglu(px, L["gate"], L["up"]),
                                     2 * INTER * HIDDEN + 8 * INTER + 2 * pm * HIDDEN + 2 * pm * INTER,
                                     4 * pm * INTER * HIDDEN, "mfma", reps=5)
-            proof["kernel"] = "gemm_k64_kernel<BM=128,BN=64,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
+            proof["kernel"] = "gemm_dma_kernel<BM=128,BN=64,NMAT=2> (fused gate|up, 2x[11008,2048] int8, 512 tokens)"
             proof["traffic"] = read_traffic("gemm_gate_up_m512") if pm == 512 else None
             result["prefill"] = {"m": pm, "value": round(tflops, 2), "unit": "TFLOP/s",
                                  "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),

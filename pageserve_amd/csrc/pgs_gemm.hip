@@ -14,7 +14,10 @@
 //    ds_read_b128 cover all 64 banks once.  All 4 waves read them as B.
 //  * Global loads run ahead of the MFMAs: one K step (LEAD = 1, predicated)
 //    or two (LEAD = 2, rotating register sets).  Weights stay in registers,
-//    activations go registers -> LDS one step before their use.
+//    activations go registers -> LDS one step before their use, or, in
+//    gemm_dma_kernel (the SwiGLU pair above 128 tokens, lm_head, and single
+//    matrices with many tiles), straight from memory into S LDS stages by
+//    the buffer unit's LDS DMA, S - 1 steps ahead and without registers.
 //  * Weight loads are ordinary cached loads: the tiles_m workgroups of one
 //    weight panel run together on one XCD and share it through its L2.
 //  * NMAT = 2 is the SwiGLU pair: gate and up blocks of the same rows are
@@ -378,6 +381,27 @@ __device__ __forceinline__ void run_steps(Step& step, int kt0, int kt1, std::int
     if (!((step(std::integral_constant<int, Is>{}, kt), ++kt < kt1) && ...)) break;
 }
 
+// f(integral_constant<J>) for J in Js, in order.
+template <typename F, int... Js>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Js...>) {
+  (f(std::integral_constant<int, Js>{}), ...);
+}
+
+// The same steps as whole unrolled blocks in a loop with a single exit, then
+// the remainder (fewer than sizeof...(Is) steps, positions 0, 1, ...) after
+// it.  For loops that read LDS filled by buffer-to-LDS DMA: at the head of a
+// loop with an exit after every step the compiler's wait insertion loses
+// track of which LDS object each DMA in flight targets and waits for all of
+// them; with one exit it keeps them apart.
+template <typename Step, int... Is>
+__device__ __forceinline__ void run_blocks(Step& step, int iters, std::integer_sequence<int, Is...>) {
+  constexpr int U = sizeof...(Is);
+  int j = 0;
+  for (; j + U <= iters; j += U) (step(std::integral_constant<int, Is>{}, j + Is), ...);
+  const int r = iters - j;
+  ((Is < r ? step(std::integral_constant<int, Is>{}, j + Is) : void()), ...);
+}
+
 constexpr int gcd2(int a, int b) { return b ? gcd2(b, a % b) : a; }
 constexpr int lcm3(int a, int b, int c) { return a / gcd2(a, b) * b / gcd2(a / gcd2(a, b) * b, c) * c; }
 
@@ -596,6 +620,207 @@ __global__ __launch_bounds__(kThreads * KG, OCC) void gemm_k64_kernel(const uint
   }
   store_tile<BN, TN, TM, NMAT, OUT_F32>(acc, a, g, M, N, m0, n0, wave, lr, lg);
 }
+// The same tile with the activations moved from HBM/L2 into LDS by the
+// buffer unit itself (buffer_load_dwordx4 ... lds, gfx950's 16-byte LDS DMA)
+// instead of through registers: S stages of [BM][64] bf16, each the target of
+// DMAs issued S - 1 K steps before its use, so an activation tile has S - 1
+// steps to arrive and costs no registers while in flight (the register path
+// could afford one step of lead, and its waves stalled at the end of every
+// step on the LDS store of the next step's activations).  Each stage is its
+// own LDS object, so the compiler's LDS-DMA tracking waits for exactly the
+// DMAs of the stage a read touches; the waits that make a stage visible to
+// the other waves are explicit: every wave waits for its own DMAs of the
+// next stage (a vmcnt count: the loop issues the same loads every step),
+// then one barrier per step.  Weights go to registers as in gemm_k64_kernel.
+// Each lane's DMA writes 16 bytes at a fixed position of its wave's 1 KiB
+// slice; the lane fetches the activation piece whose swizzled home (swz) is
+// that position.
+// 16 bytes per lane from a buffer into LDS: lane l's bytes land at lds + 16 l
+// (the LDS address is wave-uniform; it goes to M0).  A __device__ function of
+// its own: used directly in a kernel template, the builtin makes the host
+// pass drop that kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int S, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_dma_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
+  constexpr int TM = BM / 16, TN = BN / 64;
+  constexpr int WSETS = WLEAD + 1;
+  constexpr int UNROLL = lcm3(WSETS, S, 1);
+  constexpr int XS = BM * kBK;           // bf16 elements of one stage
+  constexpr int XL = BM * 8 / kThreads;  // DMA instructions per lane per stage
+  constexpr int WL = NMAT * TN;          // weight loads per lane per step
+  // (WLEAD >= S - 3: the per-step wait below counts the loads issued after
+  // a stage's DMA; the first steps' stages come from the prologue, after
+  // which only WLEAD weight steps were issued)
+  static_assert(BM % 32 == 0 && BN % 64 == 0 && XL >= 1 && S >= 2 && S <= 8 && WLEAD >= 1 && WLEAD >= S - 3,
+                "tile / pipeline");
+  __shared__ __attribute__((aligned(16))) uint16_t st0[XS];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[XS];
+  __shared__ __attribute__((aligned(16))) uint16_t st2[S > 2 ? XS : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t st3[S > 3 ? XS : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t st4[S > 4 ? XS : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t st5[S > 5 ? XS : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t st6[S > 6 ? XS : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t st7[S > 7 ? XS : 1];
+  auto stage = [&](auto I) -> uint16_t* {
+    constexpr int i = decltype(I)::value;
+    if constexpr (i == 0) return st0;
+    else if constexpr (i == 1) return st1;
+    else if constexpr (i == 2) return st2;
+    else if constexpr (i == 3) return st3;
+    else if constexpr (i == 4) return st4;
+    else if constexpr (i == 5) return st5;
+    else if constexpr (i == 6) return st6;
+    else return st7;
+  };
+
+  const GroupArgs& a = ga.g;
+  const int M = ga.M, K = ga.K;
+  // (the wave index is wave-uniform; readfirstlane makes that visible, so the
+  // DMA's LDS address -- it goes to M0 -- stays a scalar)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_n = ga.tiles / ga.tiles_m;
+  int vn, mt_all;
+  block_order(xcd_remap(blockIdx.x, ga.tiles * ga.splits), tiles_n * ga.splits, ga.tiles_m, vn, mt_all);
+  const int s = vn / tiles_n, nt_all = vn - s * tiles_n;
+  const int t = nt_all * ga.tiles_m + mt_all;
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (NMAT == 1 && i < a.n_outs && nt_all >= a.unit_begin[i]) ? i : g;
+  const int N = pick(a.n, g);
+  const int n0 = (nt_all - pick(a.unit_begin, g)) * BN;
+  const int m0 = mt_all * BM;
+  const int kb = K / kBK;
+  const int kt0 = static_cast<int>(static_cast<int64_t>(s) * kb / ga.splits);
+  const int kt1 = static_cast<int>(static_cast<int64_t>(s + 1) * kb / ga.splits);
+  const int iters = kt1 - kt0, last = kt1 - 1;
+
+  const int blk0 = n0 >> 4, blocks = (N + 15) >> 4;
+  __amdgpu_buffer_rsrc_t wres[NMAT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const int8_t* qg = (NMAT == 2) ? a.q[mat] : pick(a.q, g);
+    wres[mat] = make_rsrc(qg + static_cast<int64_t>(blk0) * kb * 1024, static_cast<int64_t>(blocks - blk0) * kb * 1024);
+  }
+  int woff[TN];
+#pragma unroll
+  for (int nt = 0; nt < TN; ++nt) woff[nt] = (wave * TN + nt) * kb * 1024 + lane * 16;
+  // activations: rows m0.. of x; rows past M read as zero
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<int64_t>(M - m0) * K * 2);
+  // DMA j of this wave fills 16-byte positions p = (wave*XL + j)*64 + lane of
+  // a stage: row p / 8, physical chunk p % 8, i.e. logical chunk
+  // (p % 8) ^ f(row), the inverse of swz
+  int xoff_g[XL];
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int p = (wave * XL + j) * 64 + lane;
+    const int row = p >> 3;
+    const int ch = (p & 7) ^ (row & 7) ^ ((row >> 3) & 1);
+    xoff_g[j] = row * K * 2 + ch * 16;
+  }
+  const int lr = lane & 15, lg = lane >> 4;
+  const int bofs0 = swz(lr, 2 * lg), bofs1 = swz(lr, 2 * lg + 1);
+
+  using WRegs = u32x4[NMAT][TN];
+  WRegs wset[WSETS];
+  auto wload = [&](int kt, WRegs& w) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int nt = 0; nt < TN; ++nt) w[mat][nt] = __builtin_amdgcn_raw_buffer_load_b128(wres[mat], woff[nt], kt * 1024, 0);
+  };
+  auto dma = [&](uint16_t* dst, int kt) {
+#pragma unroll
+    for (int j = 0; j < XL; ++j)
+      dma16(xres, dst + (wave * XL + j) * 512, xoff_g[j], kt * (kBK * 2));
+  };
+
+  f32x4 acc[NMAT][TN][TM];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) acc[mat][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const WRegs& wc, const uint16_t* stg) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* bsrc = stg + (h ? bofs1 : bofs0);
+      bf16x8 bx[TM];
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt) bx[mt] = *reinterpret_cast<const bf16x8*>(bsrc + mt * 1024);
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 aw[NMAT][TN];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) aw[mat][nt] = i8x8_to_bf16x8(wc[mat][nt][2 * h], wc[mat][nt][2 * h + 1]);
+#pragma unroll
+      for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int nt = 0; nt < TN; ++nt) acc[mat][nt][mt] = mfma16x16x32(aw[mat][nt], bx[mt], acc[mat][nt][mt]);
+    }
+  };
+  // Every wave waits for its own DMAs into the stage the next step reads
+  // (issued S - 2 steps before this one; each later step issued WL weight
+  // loads, then XL DMAs), then one barrier makes the stage visible to all
+  // and frees the stage just read for the DMA of the next step.
+  constexpr int kAfter = (S - 2) * (WL + XL);
+  constexpr int kWait = 0xF70 | (kAfter & 15) | ((kAfter >> 4) << 14);
+  static_assert(kAfter < 64, "vmcnt range");
+  auto step_barrier = [&] {
+    __builtin_amdgcn_s_waitcnt(kWait);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // Iteration j (position i of the unrolled loop): weights of j + WLEAD into
+  // set (i + WLEAD) % WSETS, DMA of j + S - 1 into stage (i + S - 1) % S
+  // (loads past the last step repeat it: in bounds, counts unchanged), the
+  // MFMAs of j on set i % WSETS and stage i % S, then the barrier.
+  auto step = [&](auto I, int j) {
+    constexpr int i = decltype(I)::value;
+    const int kt = kt0 + j;
+    wload(min(kt + WLEAD, last), wset[(i + WLEAD) % WSETS]);
+    dma(stage(std::integral_constant<int, (i + S - 1) % S>{}), min(kt + S - 1, last));
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    compute(wset[i % WSETS], stage(std::integral_constant<int, i % S>{}));
+    __builtin_amdgcn_s_setprio(0);
+    step_barrier();
+  };
+  // (the planner gives every split at least one K step; a guard on iters here
+  // costs the accumulators their registers: the compiler then spills them)
+  {
+    // prologue: stages 0 .. S-2, then weights 0 .. WLEAD-1; wait for stage 0
+    static_for([&](auto J) { dma(stage(J), min(kt0 + decltype(J)::value, last)); },
+               std::make_integer_sequence<int, S - 1>{});
+#pragma unroll
+    for (int j = 0; j < WLEAD; ++j) wload(min(kt0 + j, last), wset[j]);
+    constexpr int kPro = (S - 2) * XL + WLEAD * WL;
+    constexpr int kProWait = 0xF70 | (kPro & 15) | ((kPro >> 4) << 14);
+    static_assert(kPro < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(kProWait);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    run_blocks(step, iters, std::make_integer_sequence<int, UNROLL>{});
+    // the last steps' repeated loads (DMAs into LDS among them) land before
+    // the workgroup ends and its LDS is handed to the next one
+    __builtin_amdgcn_s_waitcnt(0xF70);
+  }
+  if (ga.splits > 1) {
+    store_partials<TN, TM, NMAT>(acc, ga, t, s, wave, lane);
+    return;
+  }
+  store_tile<BN, TN, TM, NMAT, OUT_F32>(acc, a, g, M, N, m0, n0, wave, lr, lg);
+}
+
 // Sums the split partial tiles in split order and runs the epilogue.  One
 // thread per accumulator slot (4 consecutive output rows of one token) over
 // all tiles; partial reads are coalesced 16-byte loads.
@@ -663,23 +888,38 @@ int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   return check_launch("w8a16 gemm reduce kernel");
 }
 
-// Measured on MI355X (Qwen2.5-3B projections, 512 and 2048 tokens).
-// K % 64 == 0: the buffer-load kernel with two-step weight and activation
-// leads; the SwiGLU pair at 2 waves per SIMD, single matrices at 4, or, with
-// at most two work units per CU (o / q|k|v / down_proj at 512 tokens), in two
-// K groups per workgroup, and a long K over at most one work unit per CU
-// (down_proj at 1024 tokens) in four.  Other K: the pointer kernel (SwiGLU: one-step
-// pipeline at the compiler's register budget; single matrices: two-step
-// pipeline at 4 waves per SIMD).
+template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int S, int OCC>
+int launch_dma(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  const int64_t grid = static_cast<int64_t>(ga.tiles) * ga.splits;
+  note_launch(__PRETTY_FUNCTION__, grid, ga.splits, ga.splits > 1 ? "gemm_reduce_kernel" : nullptr);
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, NMAT, OUT_F32, WLEAD, S, OCC>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kThreads), 0, st, x, ga);
+  int rc = check_launch("w8a16 gemm kernel");
+  if (rc || ga.splits == 1) return rc;
+  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
+  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
+                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
+  return check_launch("w8a16 gemm reduce kernel");
+}
+
+// Measured on MI355X (Qwen2.5-3B projections, 512, 1024 and 2048 tokens).
+// K % 64 == 0: at least two work units per CU without a K split (q|k|v, o
+// and down_proj at 2048 tokens): the LDS-DMA kernel, 4 waves per SIMD
+// (o 23.4 vs 24.6 us, q|k|v 29.5 vs 30.5 us at 2048 tokens); at most two
+// work units per CU (o / q|k|v / down_proj at 512 and 1024 tokens): the
+// buffer-load kernel in two K groups per workgroup, or, for a long K over
+// at most one work unit per CU (down_proj at 1024 tokens), four.  Other K:
+// the pointer kernel (SwiGLU: one-step pipeline at the compiler's register
+// budget; single matrices: two-step pipeline at 4 waves per SIMD).
 template <int BM, int NMAT, bool OUT_F32>
 int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   if (ga.K % kBK == 0) {
     if constexpr (NMAT == 2) return launch_k64<BM, kBN, 2, OUT_F32, 2, 2, 2>(x, ga, st);
+    const int64_t units = static_cast<int64_t>(ga.tiles) * ga.splits;
     // a long K over at most one workgroup per CU: four K groups
-    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 256 && ga.K / kBK > 64)
-      return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
-    if (static_cast<int64_t>(ga.tiles) * ga.splits <= 512) return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
-    return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 4>(x, ga, st);
+    if (units <= 256 && ga.K / kBK > 64) return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
+    if (units >= 512 && ga.splits == 1) return launch_dma<BM, kBN, 1, OUT_F32, 2, 3, 4>(x, ga, st);
+    return launch_k64<BM, kBN, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
   }
   if constexpr (NMAT == 2)
     return launch_cfg<BM, kBN, 2, OUT_F32, 1, 1>(x, ga, st);
@@ -695,7 +935,9 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
       // (each widened weight operand feeds 8 MFMAs; B operands are reused
       // across the pair's two A tiles per wave); 33..128 tokens: 64 x 64
       // tiles in two K groups
-      if (plan.bm == 128) return launch_k64<128, 64, 2, OUT_F32, 2, 1, 2>(x, ga, st);
+      // (LDS-DMA activations, three stages, 3 waves per SIMD: 46.3 vs 47.8 us
+      // at 512 tokens, 159 vs 169 us at 2048 over the register-staged kernel)
+      if (plan.bm == 128) return launch_dma<128, 64, 2, OUT_F32, 2, 3, 3>(x, ga, st);
       return launch_k64<64, 64, 2, OUT_F32, 2, 2, 1, 2>(x, ga, st);
     } else {
       // single matrices at 33..128 tokens: 64-row tiles in four K groups
@@ -704,7 +946,8 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
     }
   }
   if constexpr (NMAT == 1) {
-    if (plan.bm == 128 && plan.bn == kBN && ga.K % kBK == 0) return launch_k64<128, kBN, 1, OUT_F32, 2, 2, 2>(x, ga, st);
+    // (lm_head at 256 tokens: 155-161 vs 174-184 us with register-staged activations)
+    if (plan.bm == 128 && plan.bn == kBN && ga.K % kBK == 0) return launch_dma<128, kBN, 1, OUT_F32, 2, 3, 2>(x, ga, st);
   }
   if (plan.bm == 128) return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 gemm: no 128-token tile kernel for this shape");
   return plan.bm == 32 ? launch_bm<32, NMAT, OUT_F32>(x, ga, st) : launch_bm<64, NMAT, OUT_F32>(x, ga, st);
