@@ -96,11 +96,12 @@ constexpr int skinny_occ(int nw, int nb, int nmat, int tm) {
   return (tm == 1 && nmat == 2 && nw == 8 && nb == 2) ? 6 : 1;
 }
 
-// LDS of a kernel with xm staged tokens (slots of s chunks; the fused norm
-// adds its per-wave partial sums); at most 160 KiB per workgroup on gfx950.
+// LDS of a kernel with xm staged tokens (slots of s chunks; 16 tokens are
+// staged one batch at a time; the fused norm adds its per-wave partial sums);
+// at most 160 KiB per workgroup on gfx950.
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, bool norm) {
-  return (xm > 0 ? nw * nb * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
+  return (xm > 0 ? nw * (xm == 16 ? 1 : nb) * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
 }
 
 // Template parameters:
@@ -126,7 +127,8 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
                                                          unsigned long long* __restrict__ pairs,
                                                          const uint16_t* __restrict__ nw, float eps) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
-  static_assert(XM == 0 || (NB > 0 && K64 && 8 % XM == 0), "activation staging covers issue-once shapes");
+  static_assert(XM == 0 || (NB > 0 && K64 && (8 % XM == 0 || (XM == 16 && !NORM && !FOLD))),
+                "activation staging covers issue-once shapes");
   static_assert(!NORM || (XM > 0 && !OUT_F32), "the fused norm works on staged activations");
   static_assert(TM == 1 || (TM == 2 && !FOLD && XM == 0), "two token blocks: unfolded, direct activation loads");
   const int lane = threadIdx.x & 63;
@@ -258,10 +260,17 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
   // address, an LDS broadcast), by XPASS loads per wave.  Only this wave
   // touches its slice.  Slice layout: row (slot chunk, token) of 8 pieces,
   // rows 9 pieces apart, so that the B reads of up to eight rows (XM tokens
-  // x 2 chunks) fall on distinct banks.
+  // x 2 chunks) fall on distinct banks (and those of 16 tokens: row r starts
+  // at 144 r bytes, distinct 16-byte bank groups mod 256).  XM = 16 parks one
+  // batch at a time into a slice of one batch (PHASED): all of a wave's
+  // batches would need 9 KiB per wave, too much LDS for the resident
+  // workgroups the weight stream needs.
+  constexpr bool PHASED = XM == 16;
   constexpr int XP = XM > 0 ? NB * U * S * XM * 8 : 1;
   constexpr int XPASS = (XP + 63) / 64;
-  constexpr int XROWS = XM > 0 ? NB * U * S * XM : 1;
+  constexpr int XROWS = XM > 0 ? (PHASED ? U * S * XM : NB * U * S * XM) : 1;
+  constexpr int PPB = PHASED ? U * S * XM * 8 / 64 : 1;  // passes per batch
+  static_assert(!PHASED || PPB * 64 == U * S * XM * 8, "whole passes per batch");
   __shared__ u32x4 xst[XM > 0 ? NW * XROWS * 9 : 1];
   u32x4* const xw = xst + (XM > 0 ? wave * XROWS * 9 : 0);
 
@@ -272,7 +281,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
       const bool on = ch < ce && (K64 || ch * 64 + kgrp * 16 < K);
       const uint32_t mask = on ? 0xffffffffu : 0u;
       if constexpr (XM > 0) {
-        const u32x4* src = xw + (((j * U + u) * S + xsub) * XM + xrow) * 9 + kgrp * 2;
+        const u32x4* src = xw + ((((PHASED ? 0 : j) * U + u) * S + xsub) * XM + xrow) * 9 + kgrp * 2;
         mac(b.w[u], src[0] & mask, src[1] & mask);
       } else if constexpr (TM == 2) {
         mac2(b.w[u], b.x[u][0] & mask, b.x[u][1] & mask, b.x[u][2] & mask, b.x[u][3] & mask);
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
         xpiece[i] = tl < M ? o : u32x4{0u, 0u, 0u, 0u};  // (tokens past M: never read)
       }
     }
-    if constexpr (XM > 0) {
+    if constexpr (XM > 0 && !PHASED) {
 #pragma unroll
       for (int i = 0; i < XPASS; ++i) {
         const int p = lane + 64 * i;
@@ -377,7 +386,22 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
     // 6.28 us, q|k|v 3.36 -> 3.34)
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) mac_batch(bt[j], first + j * kStep, j);
+    for (int j = 0; j < NB; ++j) {
+      if constexpr (PHASED) {
+        // batch j's passes into the slice (the previous batch's reads of it
+        // were issued before these stores: one wave's LDS operations run in
+        // order), then its MFMAs
+#pragma unroll
+        for (int i = j * PPB; i < (j + 1) * PPB; ++i) {
+          const int p = lane + 64 * i - j * PPB * 64;
+          xw[(p >> 3) * 9 + (p & 7)] = xpiece[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+      }
+      mac_batch(bt[j], first + j * kStep, j);
+      if constexpr (PHASED) asm volatile("" ::: "memory");
+    }
     __builtin_amdgcn_s_setprio(0);
   } else {
     epi = load_epi();
@@ -523,6 +547,19 @@ int launch_kernel(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
       if (p.m == 1) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 1, false>(p, plan, st);
       if (p.m == 2) return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 2, false>(p, plan, st);
       return launch_instance<NW, U, NB, NMAT, OUT_F32, true, FOLD, 4, false>(p, plan, st);
+    }
+  }
+  // 9..16 tokens (single matrices, unfolded, issue-once batches): the same
+  // staging, one batch at a time.  A direct B load of 16 tokens touches 16
+  // activation rows (16 cache lines per KiB); a staged load covers 8 rows x
+  // 128 bytes.  Measured at 16 tokens: down_proj's paired halves 9.97 ->
+  // 8.34 us, q|k|v 4.8 -> 4.1, o_proj's halves 4.4 -> 4.2; the SwiGLU pair
+  // (each B fragment already feeds two MFMAs) 11.3 -> 11.4, so it keeps
+  // direct loads.
+  if constexpr (NB > 0 && !FOLD && NMAT == 1) {
+    if (p.k % 64 == 0 && p.m > 8 && p.m <= 16) {
+      if constexpr (skinny_lds_bytes(NW, U, NB, NMAT, 1, 16, false) <= kLdsLimit)
+        return launch_instance<NW, U, NB, NMAT, OUT_F32, true, false, 16, false>(p, plan, st);
     }
   }
   if constexpr (NB > 0 && !FOLD && NMAT == 1) {

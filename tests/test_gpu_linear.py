@@ -58,6 +58,11 @@ SHAPES = [
     # unfolded single matrices at 3..8 tokens, activations staged (4 / 8 tokens):
     # wide, 129..255 tiles, paired K halves, a long K over few tiles, 16-wave shapes
     (3, 4096, 1024), (5, 4096, 2048), (8, 2560, 1024), (6, 2048, 11008), (7, 300, 8192),
+    # unfolded single matrices at 9..16 tokens, activations staged one batch at a
+    # time: unsplit (q|k|v-, gate-like, wide), paired halves (o, down_proj), an odd
+    # chunk count over paired halves
+    (16, 2560, 2048), (16, 11008, 2048), (10, 4096, 1024), (12, 2048, 2048), (9, 2048, 11008),
+    (13, 300, 4160),
     (4, 5000, 4096), (8, 9000, 3072),
 ]
 
@@ -177,7 +182,8 @@ def test_paired_split_leaves_the_workspace_clean(gpu):
 
 @pytest.mark.parametrize("m,n,k", [(3, 1000, 1040), (8, 256, 2048), (16, 256, 2048), (2, 2048, 11008), (5, 17, 48),
                                    (20, 2048, 2048), (32, 256, 2048), (27, 300, 1040), (7, 4864, 896),
-                                   (6, 2048, 11008), (4, 4096, 1024)])
+                                   (6, 2048, 11008), (4, 4096, 1024), (12, 2048, 2048), (16, 2048, 11008),
+                                   (11, 2560, 2048)])
 def test_nonfinite_token_stays_in_its_row(gpu, m, n, k):
     """A token whose activations hold inf and nan poisons only its own
     outputs (as in x @ W^T): padding columns and the K range of another
