@@ -33,6 +33,8 @@ def _mlp_weights(gpu, seed, inter, hidden):
                                             # 128-token x 64-row tiles: split K, ragged M and N
                                             (100, 256, 4096), (300, 1000, 2048), (65, 64, 64),
                                             (33, 1000, 2048),
+                                            # 65..128 tokens: 64-token tiles, LDS-DMA activations
+                                            (80, 11008, 2048), (96, 1000, 2112),
                                             # two token blocks: unsplit, and a long K split into partials
                                             (32, 11008, 2048), (24, 1000, 8192), (21, 300, 1040)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
