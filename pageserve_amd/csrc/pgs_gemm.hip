@@ -902,6 +902,118 @@ int launch_dma(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   return check_launch("w8a16 gemm reduce kernel");
 }
 
+// A short K over few tokens in one round trip (single matrices at 33..128
+// tokens with K <= 64 NG CPG, e.g. q|k|v and o_proj of a 2048-hidden model).
+// The stepped kernels spend ~1 us per 64-k step there waiting on their own
+// pipeline (every step's loads, LDS stores and barrier on the critical path
+// of few waves) while the work per step is tiny.  Here a workgroup of 16
+// waves owns 16 tokens x 16 NT weight rows: every wave issues all of its loads
+// at once -- a sixteenth of the 16 x K activation tile by LDS DMA (each
+// lane's 16 bytes placed at their swizzled home, rows past M read as zero)
+// and its weight blocks (one 16-row tile, every NG-th 64-k chunk, CPG
+// blocks) into registers -- then one wait and one barrier, its MFMAs, and
+// the NG K groups summed through LDS in a fixed order.  NT = 4, 2 or 1
+// 16-row tiles per workgroup (NG = 16 / NT K groups).
+template <int CPG, int NT, bool OUT_F32>
+__global__ __launch_bounds__(1024) void gemm_once_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
+  constexpr int BM = 16, BN = 16 * NT, NG = 16 / NT;
+  constexpr int CH = NG * CPG;       // chunks (64 k) the activation tile holds
+  constexpr int CHUNK = BM * kBK;    // bf16 elements of one chunk block (2 KiB)
+  constexpr int SLICES = CH * CHUNK * 2 / 1024;  // 1 KiB DMA slices of the tile
+  constexpr int SPW = SLICES / 16;               // per wave
+  static_assert(SPW * 16 == SLICES && NT * NG == 16, "whole slices per wave; 16 waves");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[CH * CHUNK];
+  const GroupArgs& a = ga.g;
+  const int M = ga.M, K = ga.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = wave % NT, grp = wave / NT;  // 16-row tile, K group
+  const int tiles_n = ga.tiles / ga.tiles_m;
+  int vn, mt_all;
+  block_order(xcd_remap(blockIdx.x, ga.tiles), tiles_n, ga.tiles_m, vn, mt_all);
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PGS_MAX_GROUP; ++i) g = (i < a.n_outs && vn >= a.unit_begin[i]) ? i : g;
+  const int N = pick(a.n, g);
+  const int n0 = (vn - pick(a.unit_begin, g)) * BN;
+  const int m0 = mt_all * BM;
+  const int kb = K / kBK;  // <= CH (the planner's bound)
+
+  // activations: 16-byte position p of the tile is chunk p / 128, row
+  // (p % 128) / 8, physical piece p % 8, i.e. logical piece (p % 8) ^ f(row)
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<int64_t>(M - m0) * K * 2);
+  const int nslices = kb * CHUNK * 2 / 1024;
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int sl = wave * SPW + j;
+    if (sl < nslices) {
+      const int p = sl * 64 + lane;
+      const int c = p >> 7, row = (p >> 3) & 15, pc = p & 7;
+      const int lc = pc ^ (row & 7) ^ ((row >> 3) & 1);
+      dma16(xres, xs + sl * 512, row * K * 2 + c * 128 + lc * 16, 0);
+    }
+  }
+  // epilogue operands
+  const int lr = lane & 15, lg = lane >> 4;
+  const int nb = n0 + nt * 16 + 4 * lg;
+  const Rows4<1> e = rows4<1>(a, g, N, nb);
+  // weights, last: this wave's tile, chunks grp, grp + NG, ... (CPG of
+  // them; a chunk past K is never used)
+  const int blk0 = n0 >> 4, blocks = (N + 15) >> 4;
+  const __amdgpu_buffer_rsrc_t wres =
+      make_rsrc(pick(a.q, g) + static_cast<int64_t>(blk0) * kb * 1024, static_cast<int64_t>(blocks - blk0) * kb * 1024);
+  const int woff = nt * kb * 1024 + lane * 16;
+  u32x4 w[CPG];
+#pragma unroll
+  for (int j = 0; j < CPG; ++j) w[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, woff, (j * NG + grp) * 1024, 0);
+
+  // this wave's DMAs (and everything else but the weight loads, issued
+  // last) have landed when at most CPG loads are outstanding; the barrier
+  // then makes the whole tile visible, and each weight block is waited for
+  // only where its MFMAs use it
+  constexpr int kWait = 0xF70 | (CPG & 15) | ((CPG >> 4) << 14);
+  __builtin_amdgcn_s_waitcnt(kWait);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  const int bofs0 = swz(lr, 2 * lg), bofs1 = swz(lr, 2 * lg + 1);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int j = 0; j < CPG; ++j) {
+    const int c = j * NG + grp;
+    if (c < kb) {
+      const uint16_t* blk = xs + c * CHUNK;
+      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(blk + bofs0);
+      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(blk + bofs1);
+      acc = mfma16x16x32(i8x8_to_bf16x8(w[j][0], w[j][1]), b0, acc);
+      acc = mfma16x16x32(i8x8_to_bf16x8(w[j][2], w[j][3]), b1, acc);
+    }
+  }
+  __builtin_amdgcn_s_setprio(0);
+  // the K quarters meet in LDS (the tile's space, free after this barrier)
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(xs);
+  red[(grp * NT + nt) * 64 + lane] = acc;
+  __syncthreads();
+  if (grp != 0) return;
+  f32x4 v = red[nt * 64 + lane];
+#pragma unroll
+  for (int q = 1; q < NG; ++q) v += red[(q * NT + nt) * 64 + lane];
+  const int m = m0 + lr;
+  if (m >= M) return;
+  void* y = pick(a.y, g);
+  store_rows4<1, OUT_F32>(a, g, N, m, nb, e, v, v, y, vec_out<OUT_F32>(y, N));
+}
+
+template <int CPG, int NT, bool OUT_F32>
+int launch_once(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
+  if (ga.splits != 1 || ga.K % kBK != 0 || ga.K > 16 / NT * CPG * kBK)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 gemm: one-shot tile for K=%d", ga.K);
+  note_launch(__PRETTY_FUNCTION__, ga.tiles, 1);
+  hipLaunchKernelGGL((gemm_once_kernel<CPG, NT, OUT_F32>), dim3(static_cast<unsigned>(ga.tiles)), dim3(1024), 0, st, x, ga);
+  return check_launch("w8a16 gemm kernel");
+}
+
 // Measured on MI355X (Qwen2.5-3B projections, 512, 1024 and 2048 tokens).
 // K % 64 == 0: at least two work units per CU without a K split (q|k|v, o
 // and down_proj at 2048 tokens): the LDS-DMA kernel, 4 waves per SIMD
@@ -929,6 +1041,14 @@ int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 
 template <int NMAT, bool OUT_F32>
 int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hipStream_t st) {
+  if constexpr (NMAT == 1) {
+    // one-shot 16-token tiles (K <= 2048): 64, 32 or 16 rows in 4, 8 or 16 K groups
+    if (plan.bm == 16) {
+      if (plan.bn == 64) return launch_once<8, 4, OUT_F32>(x, ga, st);
+      if (plan.bn == 32) return launch_once<4, 2, OUT_F32>(x, ga, st);
+      return launch_once<2, 1, OUT_F32>(x, ga, st);
+    }
+  }
   if (ga.K % kBK == 0 && plan.bn == 64) {
     if constexpr (NMAT == 2) {
       // the SwiGLU pair above 128 tokens: 128 tokens x 64 rows per matrix
@@ -971,6 +1091,27 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
   auto tiles_for = [&](int bm) { return static_cast<int64_t>((m + bm - 1) / bm) * tiles_n; };
   if (mid) {
+    // a single matrix with K <= 2048: one-shot 16-token tiles of 16, 32 or 64
+    // rows, the smallest whose count fills the 256 CUs at most once (o_proj
+    // at 64 tokens 6.1 vs 9.3 us, q|k|v at 96 tokens 7.8 vs 9.2 us); more
+    // tiles than that run past one round and lose to the stepped kernel
+    // (q|k|v at 128 tokens 11.0 vs 9.2 us)
+    if (nmat == 1 && kb <= 32) {
+      for (int nt = 1; nt <= 4; nt *= 2) {
+        int tn = 0;
+        for (int i = 0; i < members; ++i) tn += (n[i] + 16 * nt - 1) / (16 * nt);
+        if (static_cast<int64_t>((m + 15) / 16) * tn <= 256) {
+          p.bm = 16;
+          p.bn = 16 * nt;
+          p.kg = 16 / nt;
+          p.tiles_m = (m + 15) / 16;
+          p.tiles_n = tn;
+          p.tiles = p.tiles_m * tn;
+          p.splits = 1;
+          return p;
+        }
+      }
+    }
     p.bm = (nmat == 1 && kb <= 64) ? 32 : 64;
     p.kg = nmat == 2 ? 2 : 4;
     p.tiles_m = (m + p.bm - 1) / p.bm;

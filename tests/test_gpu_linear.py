@@ -42,6 +42,9 @@ SHAPES = [
     (20, 48, 16), (33, 130, 32), (40, 96, 48), (40, 256, 4112), (70, 2048, 11024),
     # 33..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also split)
     (70, 2048, 11008), (128, 2048, 11008), (96, 2560, 2048), (17, 300, 128),
+    # 33..128 tokens, K <= 2048: one-shot 16-token tiles of 64 / 32 / 16 rows,
+    # ragged M and N, a one-chunk K, a K shorter than the tile holds
+    (48, 2560, 2048), (40, 1000, 1024), (100, 300, 2048), (128, 64, 64), (33, 4000, 512),
     # folded decode (8-row halves of a tile, two K chunks per MFMA, m <= 8):
     # 2m = 16 columns, an odd chunk count with a K tail, 6 tokens
     (3, 2048, 11008), (8, 130, 1040), (6, 48, 1104), (2, 2560, 2048),
@@ -92,7 +95,7 @@ def test_fp32_output(gpu, m):
     assert r["rel"] < 1e-4
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 24, 32, 64, 512])
+@pytest.mark.parametrize("m", [1, 5, 16, 24, 32, 48, 64, 96, 128, 512])
 def test_grouped_qkv_matches_separate_calls(gpu, m):
     """q/k/v (engine/model.py:168-170) in one launch: each output matches the
     oracle and its single-weight launch within tolerance.  (Not bit for bit:
