@@ -607,6 +607,19 @@ def other_configs(layers, dev, steps):
         out[f"lm_head_m{m}"] = {"us_per_launch": round(per, 2), "GB/s": round(nbytes / (per * 1e-6) / 1e9, 1),
                                 "TFLOP/s": round(2 * m * vocab * HIDDEN / (per * 1e-6) / 1e12, 1)}
         del g
+    # the greedy next token (server.py:51): logits + torch.argmax against the
+    # argmax reduced inside the projection (no logits written)
+    for m in (1, 8):
+        x = act(m, HIDDEN)
+        g, _ = capture(lambda: [hw.linear(x, out_dtype=torch.float32).argmax(dim=-1) for hw in heads * 4])
+        sep = time_graph(g, max(5, steps // 10), 2) * 1e3 / 8
+        del g
+        g, _ = capture(lambda: [Q.linear_argmax(x, hw) for hw in heads * 4])
+        fused = time_graph(g, max(5, steps // 10), 2) * 1e3 / 8
+        del g
+        same = bool(torch.equal(Q.linear_argmax(x, heads[0]), heads[0].linear(x, out_dtype=torch.float32).argmax(-1)))
+        out[f"lm_head_argmax_m{m}"] = {"fused_us": round(fused, 2), "logits_then_torch_argmax_us": round(sep, 2),
+                                       "same_indices": same}
     log("[bench] lm_head correctness gate (every row's argmax against the oracle)")
     out["lm_head_correctness"] = lm_head_gate((heads[0].q.cpu().numpy(), heads[0].scale.cpu().numpy()), gate_x,
                                               gate_logits)

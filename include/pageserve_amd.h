@@ -314,6 +314,29 @@ size_t pgs_w8a16_workspace_bytes(int64_t m, const int64_t* n, int n_outs,
 size_t pgs_w8a16_rmsnorm_workspace_bytes(int64_t m, const int64_t* n, int n_outs,
                                          int64_t k, int swiglu);
 
+/*
+ * Replaces the greedy next token of server.py:51 (int(logits[-1].argmax()),
+ * also app.py:87-93 and engine/runner.py:79) after the lm_head projection of
+ * engine/model.py:193, without writing the logits: for each of the m rows of
+ * x, idx[t] = argmax over r of y[t, r] = x[t] . (q[r] * scale[r]) (+ bias[r])
+ * in fp32 -- torch.argmax's choice: the first index of the maximum, a NaN
+ * counting as the maximum, -0.0 equal to +0.0 -- and, if vmax is not NULL,
+ * vmax[t] = y[t, idx[t]] (bit-equal to pgs_w8a16_linear's fp32 output; a
+ * canonical quiet NaN for a NaN maximum).  1 <= m <= 32 (pass only the rows
+ * whose argmax is needed, e.g. the last prompt row).  idx: int64 [m];
+ * vmax: fp32 [m].  workspace: pgs_w8a16_argmax_workspace_bytes(m, n, k)
+ * bytes (per-workgroup partial maxima, fully rewritten by every call; no
+ * zero-fill needed), 8-byte aligned.  Two launches (the projection with a
+ * per-workgroup maximum in its epilogue, then one workgroup per row).
+ */
+int pgs_w8a16_linear_argmax(const void* x, const int8_t* qp, const float* scale,
+                            const void* bias, int64_t* idx, float* vmax, int64_t m,
+                            int64_t n, int64_t k, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of pgs_w8a16_linear_argmax (0 for unsupported sizes). */
+size_t pgs_w8a16_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@ from .quantization import (  # noqa: F401
     apply_rope,
     dequantize,
     linear,
+    linear_argmax,
     linear_group,
     load_quantized,
     mlp,

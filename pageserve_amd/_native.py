@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class NativeLibraryError(RuntimeError):
@@ -74,6 +74,8 @@ SIGNATURES = {
     "pgs_w8a16_rmsnorm_swiglu": (_INT, [_VP, _VP, ctypes.c_float, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP,
                                         _SZ, _VP]),
     "pgs_w8a16_rmsnorm_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
+    "pgs_w8a16_linear_argmax": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_argmax_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
 }
 
 _lock = threading.Lock()

@@ -35,6 +35,10 @@ struct Problem {
   unsigned long long* pairs;  // zeroed pair slots (skinny two-way split), or null
   const uint16_t* norm_w;     // rms_norm weight fused in front of the linear (bf16 [k]), or null
   float eps;
+  // Row-argmax mode (fp32 single matrix, skinny kernel, no K split): instead
+  // of the outputs, workgroup b writes the key of its best output of token t
+  // to keys[b * m + t] (argmax_key); null otherwise
+  unsigned long long* keys;
 };
 
 // Largest in_features of the linear kernels: their buffer offsets
@@ -66,6 +70,8 @@ struct GemmPlan {
 };
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split);
+// workgroups of a skinny launch
+int64_t skinny_grid(const SkinnyPlan& p);
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat);
 // whether the skinny kernel can apply rms_norm to its staged activations
 // (bf16 output, m <= 4, K % 64 == 0, no K split, an issue-once shape)
@@ -128,6 +134,27 @@ __device__ __forceinline__ T* pick_early(T* const (&arr)[L], int g) {
 #pragma unroll
   for (int i = 1; i < L; ++i) r = (g == i) ? v[i] : r;
   return (T*)r;
+}
+
+// Row-argmax key of output `row` with value f: ordered as (f, then smaller
+// row) under unsigned comparison, so that the maximum key is torch.argmax's
+// choice -- the first index of the maximum, every NaN counting as the
+// maximum -- and max is exact, commutative and associative (any reduction
+// order gives the same key).  -0.0 counts as +0.0.  The high word maps the
+// float's bits monotonically onto unsigned order; the low word is the
+// row's complement.  Key 0 is below every output's key.
+__device__ __forceinline__ unsigned long long argmax_key(float f, uint32_t row) {
+  const uint32_t b = __float_as_uint(f == 0.f ? 0.f : f);
+  const uint32_t hi = f != f ? 0xffffffffu : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  return (static_cast<unsigned long long>(hi) << 32) | (0xffffffffu - row);
+}
+__device__ __forceinline__ float argmax_key_value(unsigned long long key) {
+  const uint32_t hi = static_cast<uint32_t>(key >> 32);
+  if (hi == 0xffffffffu) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
+}
+__device__ __forceinline__ uint32_t argmax_key_row(unsigned long long key) {
+  return 0xffffffffu - static_cast<uint32_t>(key);
 }
 
 // Workgroup b of a grid of `total` runs on XCD b % 8 (round robin over the

@@ -298,3 +298,111 @@ extern "C" int pgs_w8a16_rmsnorm_swiglu(const void* x, const void* norm_weight, 
   return swiglu_impl(fn, x, q_gate, s_gate, q_up, s_up, act, m, n, k, workspace, workspace_bytes_, stream,
                      norm_weight, eps);
 }
+
+// ---------------------------------------------------------------------------
+// Row argmax of the logits (the greedy next token), without writing them
+// ---------------------------------------------------------------------------
+
+namespace pgs {
+namespace {
+
+constexpr int kArgmaxMaxM = kSkinnyMaxM;
+
+// One workgroup per token: the maximum of the launch's per-workgroup keys
+// (exact and order-free), decoded to the row and its logit.  Each thread
+// keeps four loads in flight (a lm_head launch leaves ~19000 keys per token).
+constexpr int kArgmaxThreads = 1024;
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_reduce_kernel(const unsigned long long* __restrict__ keys,
+                                                                       int groups, int M, int64_t* __restrict__ idx,
+                                                                       float* __restrict__ vmax) {
+  const int mm = blockIdx.x;
+  unsigned long long best[4] = {0, 0, 0, 0};
+  for (int b0 = threadIdx.x; b0 < groups; b0 += 4 * kArgmaxThreads) {
+    unsigned long long k[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = b0 + i * kArgmaxThreads;
+      k[i] = b < groups ? keys[static_cast<int64_t>(b) * M + mm] : 0ull;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) best[i] = k[i] > best[i] ? k[i] : best[i];
+  }
+  unsigned long long bb = best[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) bb = best[i] > bb ? best[i] : bb;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(bb), off);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(bb >> 32), off);
+    const unsigned long long other = (static_cast<unsigned long long>(hi) << 32) | lo;
+    bb = other > bb ? other : bb;
+  }
+  __shared__ unsigned long long part[kArgmaxThreads / 64];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = bb;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  unsigned long long best_all = part[0];
+#pragma unroll
+  for (int w = 1; w < kArgmaxThreads / 64; ++w) best_all = part[w] > best_all ? part[w] : best_all;
+  const unsigned long long best0 = best_all;
+  idx[mm] = static_cast<int64_t>(argmax_key_row(best0));
+  if (vmax) vmax[mm] = argmax_key_value(best0);
+}
+
+// the argmax call's plan: the fp32 linear's skinny plan without a K split
+SkinnyPlan argmax_plan(int m, int n, int k) { return plan_skinny(m, k, 1, (n + 15) / 16, false); }
+
+}  // namespace
+}  // namespace pgs
+
+extern "C" size_t pgs_w8a16_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m < 1 || m > kArgmaxMaxM || n < 1 || n > 0x7fffffff || k < 1 || k > kMaxK) return 0;
+  const SkinnyPlan sp = argmax_plan(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k));
+  return static_cast<size_t>(skinny_grid(sp)) * static_cast<size_t>(m) * sizeof(unsigned long long);
+}
+
+extern "C" int pgs_w8a16_linear_argmax(const void* x, const int8_t* q, const float* scale, const void* bias,
+                                       int64_t* idx, float* vmax, int64_t m, int64_t n, int64_t k, void* workspace,
+                                       size_t workspace_bytes_, void* stream) {
+  const char* fn = "pgs_w8a16_linear_argmax";
+  int rc = check_common(fn, x, m, k);
+  if (rc) return rc;
+  if (m < 1 || m > kArgmaxMaxM)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: m=%lld rows; 1..%d are supported (pass the rows whose argmax is needed)",
+                fn, (long long)m, kArgmaxMaxM);
+  if (n < 1 || k < 1) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: n=%lld, k=%lld must be positive", fn, (long long)n,
+                                  (long long)k);
+  rc = check_member(fn, q, scale, bias, idx, n, m, k);
+  if (rc) return rc;
+  if (!aligned(idx, 8) || !aligned(vmax, 4)) return fail(PGS_ERR_MISALIGNED, "%s: idx / vmax misaligned", fn);
+  const size_t need = pgs_w8a16_argmax_workspace_bytes(m, n, k);
+  if (!workspace || workspace_bytes_ < need)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes_, need);
+  if (!aligned(workspace, 8)) return fail(PGS_ERR_MISALIGNED, "%s: workspace must be 8-byte aligned", fn);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if ((rc = require_device(fn, st))) return rc;
+  Problem p{};
+  p.x = reinterpret_cast<const uint16_t*>(x);
+  p.m = static_cast<int>(m);
+  p.k = static_cast<int>(k);
+  p.nmat = 1;
+  p.out_f32 = true;
+  p.keys = static_cast<unsigned long long*>(workspace);
+  p.args.n_outs = 1;
+  for (int i = 0; i < PGS_MAX_GROUP; ++i) {
+    p.args.q[i] = q;
+    p.args.scale[i] = scale;
+    p.args.bias[i] = i == 0 ? reinterpret_cast<const uint16_t*>(bias) : nullptr;
+    p.args.y[i] = workspace;  // (not written in this mode)
+    p.args.res[i] = nullptr;
+    p.args.n[i] = i == 0 ? static_cast<int32_t>(n) : 0;
+    p.args.unit_begin[i] = 0;
+  }
+  const SkinnyPlan sp = argmax_plan(p.m, static_cast<int>(n), p.k);
+  for (int i = 1; i <= PGS_MAX_GROUP; ++i) p.args.unit_begin[i] = sp.tiles;
+  if ((rc = launch_skinny(p, sp, st))) return rc;
+  const int64_t groups = skinny_grid(sp);
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(static_cast<unsigned>(m)), dim3(kArgmaxThreads), 0, st,
+                     static_cast<const unsigned long long*>(workspace), static_cast<int>(groups), p.m, idx, vmax);
+  return check_launch("w8a16 argmax reduce kernel");
+}

@@ -125,7 +125,8 @@ template <int NW, int U, int NB, int NMAT, bool OUT_F32, bool K64, bool FOLD, in
 __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
                                                          int K, int splits, float* __restrict__ partials,
                                                          unsigned long long* __restrict__ pairs,
-                                                         const uint16_t* __restrict__ nw, float eps) {
+                                                         const uint16_t* __restrict__ nw, float eps,
+                                                         unsigned long long* __restrict__ keys) {
   static_assert(!FOLD || NMAT == 1, "folding serves single matrices");
   static_assert(XM == 0 || (NB > 0 && K64 && (8 % XM == 0 || (XM == 16 && !NORM && !FOLD))),
                 "activation staging covers issue-once shapes");
@@ -422,25 +423,52 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
   }
   __syncthreads();
 
-  if (idx >= nout) return;
+  const bool live = idx < nout;
   // token mm is column mm % 16 of block mm / 16
   const int ln = acc_lane(FOLD ? oi & 7 : oi, mm & 15), r = oi & 3, tb = TM == 2 ? mm >> 4 : 0;
   float v[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
     float t = 0.f;
+    if (live) {
 #pragma unroll
-    for (int w = 0; w < NW; ++w) t += red[w][mat * TM + tb][ln][r];
-    if constexpr (FOLD) {
-      // the second chunk of every slot: C[r + 8][mm + M]
-      const int ln2 = acc_lane((oi & 7) + 8, mm + M);
-      float t2 = 0.f;
+      for (int w = 0; w < NW; ++w) t += red[w][mat * TM + tb][ln][r];
+      if constexpr (FOLD) {
+        // the second chunk of every slot: C[r + 8][mm + M]
+        const int ln2 = acc_lane((oi & 7) + 8, mm + M);
+        float t2 = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) t2 += red[w][mat * TM][ln2][r];
-      t += t2;
+        for (int w = 0; w < NW; ++w) t2 += red[w][mat * TM][ln2][r];
+        t += t2;
+      }
     }
     v[mat] = t;
   }
+  if constexpr (NMAT == 1 && OUT_F32) {
+    if (keys) {
+      // Row-argmax mode: the fp32 output the epilogue would store (scale,
+      // bias), its key, the maximum over the token's outputs in this
+      // workgroup (consecutive threads: 8 folded, 16 otherwise, within one
+      // wave), one key per token and workgroup.
+      unsigned long long key = 0;
+      if (live && has_out) {
+        float out = v[0] * epi.s[0];
+        if (pick_early(a.bias, g)) out += bf16_bits_to_f32(epi.bias);
+        key = argmax_key(out, static_cast<uint32_t>(row0 + oi));
+      }
+      constexpr int G = FOLD ? 8 : 16;
+#pragma unroll
+      for (int off = 1; off < G; off <<= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), off);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(key >> 32), off);
+        const unsigned long long other = (static_cast<unsigned long long>(hi) << 32) | lo;
+        key = other > key ? other : key;
+      }
+      if (live && (idx & (G - 1)) == 0) keys[static_cast<int64_t>(blockIdx.x) * M + mm] = key;
+      return;
+    }
+  }
+  if (!live) return;
   if (NMAT == 1 && pairs) {
     // The two K halves of this tile meet in one 64-bit slot per output.
     // The first to arrive leaves (1, its partial); the second takes it,
@@ -501,7 +529,8 @@ int launch_instance(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   unsigned long long* pairs = plan.pair ? p.pairs : nullptr;
   note_launch(__PRETTY_FUNCTION__, grid, plan.splits, plan.splits > 1 && !plan.pair ? "skinny_reduce_kernel" : nullptr);
   hipLaunchKernelGGL((skinny_kernel<NW, U, NB, NMAT, OUT_F32, K64, FOLD, XM, NORM, TM>), dim3(static_cast<unsigned>(grid)),
-                     dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs, p.norm_w, p.eps);
+                     dim3(64 * NW), 0, st, p.x, p.args, p.m, p.k, plan.splits, p.partials, pairs, p.norm_w, p.eps,
+                     p.keys);
   return check_launch("w8a16 skinny kernel");
 }
 
@@ -688,6 +717,8 @@ bool skinny_norm_fusable(const SkinnyPlan& p, int m, int k, bool out_f32, int nm
   return sh.nb > 0 && skinny_lds_bytes(sh.nw, sh.u, sh.nb, nmat, p.fold ? 2 : 1, m == 1 ? 1 : m == 2 ? 2 : 4, true) <=
                           kLdsLimit;
 }
+
+int64_t skinny_grid(const SkinnyPlan& p) { return static_cast<int64_t>(p.tiles) * (p.fold ? 2 : p.splits); }
 
 size_t skinny_partial_bytes(const SkinnyPlan& p, int nmat) {
   return (p.splits > 1 && !p.pair) ? static_cast<size_t>(p.tiles) * p.splits * nmat * 256 * p.tm * sizeof(float) : 0;

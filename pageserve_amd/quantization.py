@@ -351,6 +351,52 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
                                       0.0, ws, ws_bytes)[0]
 
 
+def linear_argmax(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
+                  return_values: bool = False):
+    """``F.linear(x, W, bias).float().argmax(-1)`` -- the greedy next token
+    of server.py:51 after the lm_head of engine/model.py:193 -- without
+    writing the logits: the fp32 logits (as :func:`linear` with
+    ``out_dtype=torch.float32`` computes them) are reduced to their row
+    argmax inside the projection (torch.argmax's choice: the first index of
+    the maximum, NaN counting as the maximum).  x: bf16 [..., K] with at most
+    32 rows (pass only the rows whose argmax is needed, e.g. ``h[-1:]``).
+    Returns int64 indices of shape x.shape[:-1], and with ``return_values``
+    also the fp32 maxima."""
+    if weight.device.type != "cuda":
+        raise RuntimeError("linear_argmax: the weight must be on a ROCm GPU")
+    q, s, n, k, dev = weight._launch_operands()
+    if not isinstance(x, torch.Tensor) or x.device != dev:
+        raise ValueError(f"linear_argmax: input must be on {dev}")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"linear_argmax: the W8A16 kernels take bf16 activations, got {x.dtype}")
+    if x.dim() < 1 or x.shape[-1] != k:
+        raise ValueError(f"linear_argmax: input has {x.shape[-1] if x.dim() else 0} features, weight expects {k}")
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous().clone()
+    m = x2.shape[0]
+    if bias is not None:
+        if bias.device != dev or bias.dtype != torch.bfloat16 or bias.numel() != n:
+            raise ValueError(f"linear_argmax: bias must be a bf16 [{n}] tensor on {dev}")
+        bias = bias.reshape(n).contiguous()
+    idx = torch.empty(m, dtype=torch.int64, device=dev)
+    vmax = torch.empty(m, dtype=torch.float32, device=dev) if return_values else None
+    lib = _native.load()
+    need = lib.pgs_w8a16_argmax_workspace_bytes(m, n, k)
+    if need == 0:
+        raise ValueError(f"linear_argmax: {m} rows; 1..32 are supported (pass the rows whose argmax is needed)")
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    with _on_device(dev):
+        rc = lib.pgs_w8a16_linear_argmax(_ptr(x2), _ptr(q), _ptr(s), _ptr(bias) if bias is not None else None,
+                                         _ptr(idx), _ptr(vmax) if vmax is not None else None, m, n, k, _ptr(ws),
+                                         need, ctypes.c_void_p(_raw_stream(dev)))
+    check(rc, "linear_argmax")
+    shape = x.shape[:-1]
+    if return_values:
+        return idx.reshape(shape), vmax.reshape(shape)
+    return idx.reshape(shape)
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``rms_norm(x, weight, eps)`` of engine/model.py:29-34 as one kernel:
     h = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))), the mean in fp32.

@@ -54,3 +54,81 @@ def test_lm_head_logits_and_argmax(gpu, lm_head, m):
     np.testing.assert_array_equal(O.argmax_rows(got), O.argmax_rows(ref))
     # and through torch's own argmax on the GPU, as the serving loop takes it
     np.testing.assert_array_equal(logits.argmax(dim=-1).cpu().numpy(), O.argmax_rows(ref))
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_fused_argmax_lm_head(gpu, lm_head, m):
+    """Q.linear_argmax (the argmax reduced inside the projection, no logits
+    written) on the full lm_head: every row's index equals the oracle's
+    argmax (decided: top-2 gap above twice the kernel's logit error) and
+    torch's argmax of the fp32 logits of Q.linear, and the returned maximum
+    is bit-equal to that logit."""
+    qw, q, s = lm_head
+    x = activations(177 + m, m, HIDDEN)
+    xs = bf16_gpu(x, gpu)
+    idx, vmax = Q.linear_argmax(xs, qw, return_values=True)
+    assert idx.dtype == torch.int64 and idx.shape == (m,) and vmax.dtype == torch.float32
+    logits = qw.linear(xs, out_dtype=torch.float32)
+    ref = _oracle_blocked(x, q, s)
+    worst = float(np.abs(to_np(logits) - ref).max())
+    assert (O.top2_gap(ref) > 2 * worst).all()
+    np.testing.assert_array_equal(idx.cpu().numpy(), O.argmax_rows(ref))
+    np.testing.assert_array_equal(idx.cpu().numpy(), logits.argmax(dim=-1).cpu().numpy())
+    picked = logits.gather(1, idx.view(-1, 1)).view(-1)
+    assert torch.equal(vmax.view(torch.int32), picked.view(torch.int32))
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 12, 16, 17, 24, 32])
+def test_fused_argmax_every_plan(gpu, m):
+    """Every skinny plan the argmax rides on (folded at 1..2 tokens, staged
+    3..8 and 9..16, two token blocks 17..32), with a bias and a ragged
+    vocabulary: indices equal torch's argmax of the same kernel's fp32
+    logits, maxima bit-equal, and both equal the oracle's where decided."""
+    n, k = 5000 + 8, 2048
+    rng = np.random.default_rng(4242 + m)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    b = O.round_to_bf16(rng.standard_normal(n).astype(np.float32))
+    q, s = O.quantize_per_channel(w)
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu))
+    x = activations(500 + m, m, k)
+    xs, bt = bf16_gpu(x, gpu), bf16_gpu(b, gpu)
+    idx, vmax = Q.linear_argmax(xs, qw, bt, return_values=True)
+    logits = qw.linear(xs, bt, out_dtype=torch.float32)
+    np.testing.assert_array_equal(idx.cpu().numpy(), logits.argmax(dim=-1).cpu().numpy())
+    assert torch.equal(vmax.view(torch.int32), logits.gather(1, idx.view(-1, 1)).view(-1).view(torch.int32))
+    ref = O.linear(x, q, s, b)
+    decided = O.top2_gap(ref) > 2 * float(np.abs(to_np(logits) - ref).max())
+    np.testing.assert_array_equal(idx.cpu().numpy()[decided], O.argmax_rows(ref)[decided])
+
+
+def test_fused_argmax_ties_and_nan(gpu):
+    """torch.argmax's choices: duplicated weight rows give equal logits and
+    the first index wins; a token whose activations hold a NaN has all-NaN
+    logits and gets index 0 (NaN counts as the maximum); other tokens are
+    unaffected."""
+    n, k = 700, 1024
+    rng = np.random.default_rng(99)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    # rows 611 and 613 copy row 600, whose scale is then the largest
+    w[600] *= 4.0
+    w[611] = w[600]
+    w[613] = w[600]
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu))
+    x = np.zeros((3, k), dtype=np.float32)
+    x[0] = O.round_to_bf16(np.sign(w[600]).astype(np.float32))  # aligns with row 600 (and its copies)
+    x[1] = x[0]
+    x[1, 5] = np.nan
+    x[2] = -x[0]
+    xs = bf16_gpu(x, gpu)
+    idx, vmax = Q.linear_argmax(xs, qw, return_values=True)
+    logits = qw.linear(xs, out_dtype=torch.float32)
+    assert int(idx[0]) == 600 and float(logits[0, 611]) == float(logits[0, 600])
+    assert int(idx[1]) == 0 and torch.isnan(vmax[1])
+    assert int(idx[2]) == int(logits[2].argmax())
+    np.testing.assert_array_equal(idx.cpu().numpy()[[0, 2]], logits.argmax(dim=-1).cpu().numpy()[[0, 2]])
+
+
+def test_fused_argmax_rejects_too_many_rows(gpu, lm_head):
+    qw, _, _ = lm_head
+    with pytest.raises(ValueError, match="1..32"):
+        Q.linear_argmax(bf16_gpu(activations(3, 33, HIDDEN), gpu), qw)
