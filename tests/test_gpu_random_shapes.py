@@ -128,3 +128,52 @@ def test_random_fused_norm(gpu, i):
         qg, qu = O.quantize_per_channel(wg), O.quantize_per_channel(wu)
         report(to_np(act), O.swiglu(h, *qg, *qu), k, what, acc=O.swiglu_acc(h, *qg, *qu, dx=dh))
         assert torch.equal(Q.rmsnorm_swiglu(xet, wt, eps, g, u), Q.swiglu(Q.rmsnorm(xet, wt, eps), g, u)), what
+
+
+# the fused row argmax of the lm_head (server.py:51 after engine/model.py:193):
+# random token counts over every skinny plan it rides on (1..32), ragged
+# vocabularies, K with and without K % 64 == 0, bias on and off.  The checks
+# hold for any summation order (O.acc_bound bounds every fp32 evaluation):
+# the returned maximum lies within the bound of the exact logit at the
+# returned index, that index can be the maximum of some evaluation within
+# the bounds, and where the winner is decided it is the oracle's argmax.
+ARGMAX_CASES = int(os.environ.get("PGS_RANDOM_ARGMAX_CASES", "16"))
+
+
+def _argmax_case(i: int):
+    rng = np.random.default_rng(40_000 + i)
+    m = int(rng.integers(1, 33))
+    k = 16 * int(rng.integers(1, 200))
+    if i % 2 == 0:
+        k = 64 * max(1, k // 64)
+    n = int(rng.integers(1, 9000))
+    while m * n * k > MAX_WORK:
+        n = max(1, n // 2)
+    return m, n, k, bool(rng.integers(0, 2))
+
+
+@pytest.mark.parametrize("i", range(ARGMAX_CASES))
+def test_random_argmax(gpu, i):
+    m, n, k, bias = _argmax_case(i)
+    what = f"argmax case {i}: m={m} n={n} k={k} bias={bias}"
+    rng = np.random.default_rng(41_000 + i)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    b = O.round_to_bf16(rng.standard_normal(n).astype(np.float32)) if bias else None
+    x = activations(42_000 + i, m, k)
+    q, s = O.quantize_per_channel(w)
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(gpu))
+    idx, vmax = Q.linear_argmax(bf16_gpu(x, gpu), qw, bf16_gpu(b, gpu) if bias else None, return_values=True)
+    idx, vmax = idx.cpu().numpy(), vmax.cpu().numpy().astype(np.float64)
+    exact = np.asarray(x, np.float64) @ O.dequantize(q, s, "f32").astype(np.float64).T
+    if bias:
+        exact = exact + np.asarray(b, np.float64).reshape(1, -1)
+    acc = O.acc_bound(x, q, s, b)
+    rows = np.arange(m)
+    assert idx.shape == (m,) and np.all((idx >= 0) & (idx < n)), what
+    assert np.all(np.abs(vmax - exact[rows, idx]) <= acc[rows, idx]), what
+    assert np.all(exact[rows, idx] + acc[rows, idx] >= (exact - acc).max(axis=1)), what
+    best = O.argmax_rows(exact)
+    lo = exact[rows, best] - acc[rows, best]
+    others = np.where(np.arange(n)[None, :] == best[:, None], -np.inf, exact + acc)
+    decided = lo > others.max(axis=1) if n > 1 else np.ones(m, bool)
+    np.testing.assert_array_equal(idx[decided], best[decided], err_msg=what)
