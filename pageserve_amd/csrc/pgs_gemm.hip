@@ -1131,6 +1131,12 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   // 2048] at 256 tokens 165-176 vs 173-184 us; at 320..1376 tiles they are
   // no faster or slower: q|k|v at 2048 tokens 32.5 vs 29.3 us)
   if (nmat == 1 && k % kBK == 0 && p.bn == kBN && m >= 256 && tiles_for(128) >= 2048) p.bm = 128;
+  // a long K (down_proj) from 1536 tokens: 128 x 128 tiles, split K until
+  // 512 workgroups (down_proj [2048, 11008] at 1536 tokens 78.7 vs 87-90 us
+  // with four splits, at 2048 94.5 vs 99-104 us with two; at 1024 tokens
+  // within noise of the K-group plan below, which keeps that range)
+  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m >= 1536;
+  if (long128) p.bm = 128;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K
   if (nmat == 1 && p.bm == 64 && kb <= 64 && tiles_for(64) < 256) p.bm = 32;
@@ -1138,6 +1144,10 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   p.tiles_n = tiles_n;
   p.tiles = p.tiles_m * p.tiles_n;
   p.splits = 1;
+  if (long128) {
+    while (p.splits < 4 && static_cast<int64_t>(p.tiles) * p.splits < 512) p.splits *= 2;
+    return p;
+  }
   // fewer than 256 output tiles: split K until about four workgroups per CU,
   // keeping >= 32 K steps per split (>= 8 when there are very few tiles).
   // From 256 tiles on, K groups inside the workgroup beat a split and its

@@ -324,3 +324,44 @@ def test_four_k_group_plan(gpu):
     plan = _plan_kernel()
     assert kg4 in plan and "splits=1" in plan, plan
     report(to_np(out), O.linear(x, q, s, b), k, "kg4 no workspace", acc=O.acc_bound(x, q, s, b))
+
+
+def test_long_k_128_tile_plan(gpu):
+    """From 1536 tokens a long K (more than 64 steps of 64) runs 128 x 128
+    LDS-DMA tiles with the K split until 512 workgroups (launch_dma<128, 128,
+    1, *, 2, 3, 2> plus the reduce kernel): a ragged few-tile shape (four
+    splits) against the full oracle, down_proj's shape at 2048 tokens (two
+    splits) on sampled rows, and the C ABI without a workspace, which keeps
+    the unsplit plan."""
+    import ctypes
+
+    from pageserve_amd import _native
+
+    t128 = "BM = 128, BN = 128, NMAT = 1, OUT_F32 = false, WLEAD = 2, S = 3, OCC = 2"
+    m, n, k = 1536, 300, 4160
+    qw, q, s, x, b = _problem(gpu, 7721, m, n, k, bias=True)
+    xt, bt = bf16_gpu(x, gpu), bf16_gpu(b, gpu)
+    y = to_np(qw.linear(xt, bt))
+    plan = _plan_kernel()
+    assert t128 in plan and "splits=4" in plan and "gemm_reduce_kernel" in plan, plan
+    report(y, O.linear(x, q, s, b), k, "128 tile m=1536", acc=O.acc_bound(x, q, s, b))
+
+    lib = _native.load()
+    qp, sc = qw._kernel_operands()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.pgs_w8a16_linear(ctypes.c_void_p(xt.data_ptr()), ctypes.c_void_p(qp.data_ptr()),
+                              ctypes.c_void_p(sc.data_ptr()), ctypes.c_void_p(bt.data_ptr()),
+                              ctypes.c_void_p(out.data_ptr()), 1, m, n, k, None, 0, ctypes.c_void_p(stream))
+    assert rc == 0, lib.pgs_last_error()
+    plan = _plan_kernel()
+    assert t128 not in plan and "splits=1" in plan, plan
+    report(to_np(out), O.linear(x, q, s, b), k, "no workspace m=1536", acc=O.acc_bound(x, q, s, b))
+
+    m, n, k = 2048, 2048, 11008
+    qw, q, s, x, _ = _problem(gpu, 7731, m, n, k)
+    y = to_np(qw.linear(bf16_gpu(x, gpu)))
+    plan = _plan_kernel()
+    assert t128 in plan and "splits=2" in plan, plan
+    rows = np.concatenate([np.random.default_rng(5).choice(m, 40, replace=False), [0, 127, 128, m - 1]])
+    report(y[rows], O.linear(x[rows], q, s), k, "128 tile m=2048", acc=O.acc_bound(x[rows], q, s))
