@@ -1131,11 +1131,11 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   // 2048] at 256 tokens 165-176 vs 173-184 us; at 320..1376 tiles they are
   // no faster or slower: q|k|v at 2048 tokens 32.5 vs 29.3 us)
   if (nmat == 1 && k % kBK == 0 && p.bn == kBN && m >= 256 && tiles_for(128) >= 2048) p.bm = 128;
-  // a long K (down_proj) from 1536 tokens: 128 x 128 tiles, split K until
-  // 512 workgroups (down_proj [2048, 11008] at 1536 tokens 78.7 vs 87-90 us
-  // with four splits, at 2048 94.5 vs 99-104 us with two; at 1024 tokens
-  // within noise of the K-group plan below, which keeps that range)
-  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m >= 1536;
+  // a long K (down_proj) above 1024 tokens: 128 x 128 tiles, split K until
+  // 512 workgroups (down_proj [2048, 11008] at 1280 tokens 69.8 vs 79.3 us
+  // and at 1536 78.7 vs 87-90 us with four splits, at 2048 94.5 vs 99-104 us
+  // with two; at 1024 tokens and below within noise of the plans below)
+  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m > 1024;
   if (long128) p.bm = 128;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K

@@ -327,7 +327,7 @@ def test_four_k_group_plan(gpu):
 
 
 def test_long_k_128_tile_plan(gpu):
-    """From 1536 tokens a long K (more than 64 steps of 64) runs 128 x 128
+    """Above 1024 tokens a long K (more than 64 steps of 64) runs 128 x 128
     LDS-DMA tiles with the K split until 512 workgroups (launch_dma<128, 128,
     1, *, 2, 3, 2> plus the reduce kernel): a ragged few-tile shape (four
     splits) against the full oracle, down_proj's shape at 2048 tokens (two
