@@ -35,6 +35,9 @@ def _mlp_weights(gpu, seed, inter, hidden):
                                             (33, 1000, 2048),
                                             # 65..128 tokens: 64-token tiles, LDS-DMA activations
                                             (80, 11008, 2048), (96, 1000, 2112),
+                                            # above 128 tokens with a last 128-token tile at most
+                                            # half full: 64-token tiles
+                                            (160, 11008, 2048), (320, 1000, 2112),
                                             # two token blocks: unsplit, and a long K split into partials
                                             (32, 11008, 2048), (24, 1000, 8192), (21, 300, 1040)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
