@@ -1113,6 +1113,9 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
       }
     }
     p.bm = (nmat == 1 && kb <= 64) ? 32 : 64;
+    // the SwiGLU pair above 96 tokens: one 128-token tile row, each weight
+    // panel read once (128 tokens 21.9 vs 23.5 us; at 96 tokens within noise)
+    if (nmat == 2 && m > 96) p.bm = 128;
     p.kg = nmat == 2 ? 2 : 4;
     p.tiles_m = (m + p.bm - 1) / p.bm;
     p.tiles_n = tiles_n;
