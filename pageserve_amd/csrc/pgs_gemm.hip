@@ -1051,15 +1051,15 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
   }
   if (ga.K % kBK == 0 && plan.bn == 64) {
     if constexpr (NMAT == 2) {
-      // the SwiGLU pair above 128 tokens: 128 tokens x 64 rows per matrix
-      // (each widened weight operand feeds 8 MFMAs; B operands are reused
-      // across the pair's two A tiles per wave); 33..128 tokens: 64 x 64
-      // tiles in two K groups
+      // the SwiGLU pair in 128-token tiles (the planner's choice above 96
+      // tokens): 128 tokens x 64 rows per matrix (each widened weight operand
+      // feeds 8 MFMAs; B operands are reused across the pair's two A tiles
+      // per wave)
       // (LDS-DMA activations, three stages, 3 waves per SIMD: 46.3 vs 47.8 us
       // at 512 tokens, 159 vs 169 us at 2048 over the register-staged kernel)
       if (plan.bm == 128) return launch_dma<128, 64, 2, OUT_F32, 2, 3, 3>(x, ga, st);
-      // 65..128 tokens: LDS-DMA activations, four stages (80 / 96 / 112 / 128
-      // tokens: 20.5 / 21.0 / 21.6 / 22.0 vs 22.9 / 23.9 / 23.2 / 23.0 us);
+      // 64-token tiles above 64 tokens: LDS-DMA activations, four stages (80
+      // / 96 tokens: 20.5 / 21.0 vs 22.9 / 23.9 us for the two-K-group kernel);
       // at 64 tokens and below the two-K-group kernel is as fast
       if (ga.M > 64) return launch_dma<64, 64, 2, OUT_F32, 3, 4, 3>(x, ga, st);
       return launch_k64<64, 64, 2, OUT_F32, 2, 2, 1, 2>(x, ga, st);
