@@ -167,11 +167,11 @@ int pgs_w8a16_linear(const void* x, const int8_t* qp, const float* scale,
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Same arguments, launch plan
  * and results as pgs_w8a16_linear with a workspace, but the K-split scratch
- * (pair slots, partial tiles) is a fixed 32 MiB device array inside the
+ * (pair slots, partial tiles) is a fixed 64 MiB device array inside the
  * library, one per GPU, held until the process ends; the call allocates
  * nothing and frees nothing.  A shape whose plan needs more scratch than that
  * returns PGS_ERR_INVALID_ARGUMENT (every projection of a 2048-hidden /
- * 11008-intermediate model up to 2048 tokens needs at most 24.5 MiB).  Every
+ * 11008-intermediate model up to 2048 tokens needs at most 60.5 MiB).  Every
  * call on one GPU shares the array: calls that overlap on one GPU (other
  * streams, concurrently replayed graphs) race; stream-ordered calls do not.
  * The first call on a device must have that device current.

@@ -14,9 +14,10 @@ namespace pgs {
 namespace {
 
 // The largest workspace any launch plan of a 2048-hidden / 11008-intermediate
-// model needs at up to 2048 tokens is 24.5 MiB (down_proj at 384 and 768
-// tokens); plans that need more are rejected.
-constexpr size_t kScratchBytes = 32u << 20;
+// model needs at up to 2048 tokens is 60.5 MiB (down_proj at 1793 to 1920
+// tokens: 240 tiles of 128 x 128, K split 4, plus the pair slots); plans that
+// need more are rejected.
+constexpr size_t kScratchBytes = 64u << 20;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 

@@ -43,9 +43,11 @@ def _reference_call(lib, x, qp, sc, b, y, m, n, k, stream):
 
 # (m, n, k): down_proj at 200 tokens (split-K partials, 16.5 MiB) then o_proj
 # at 9 tokens (pair slots); down_proj at 5 tokens (pair slots) then 1 token
-# (folded, no scratch); a ragged tiled split then a smaller one
+# (folded, no scratch); a ragged tiled split then a smaller one; down_proj at
+# 1920 tokens (128 x 128 tiles split four ways, 60.5 MiB, the largest of the
+# model's shapes) then 1280 tokens (the same plan, 40.5 MiB)
 PAIRS = [((200, 2048, 11008), (9, 2048, 2048)), ((5, 2048, 11008), (1, 2048, 11008)),
-         ((150, 300, 4160), (40, 200, 4160))]
+         ((150, 300, 4160), (40, 200, 4160)), ((1920, 2048, 11008), (1280, 2048, 11008))]
 
 
 @pytest.mark.parametrize("first,second", PAIRS)
@@ -75,10 +77,10 @@ def test_noalloc_equals_the_workspace_entry_point(gpu, first, second):
 
 def test_noalloc_rejects_plans_beyond_its_scratch(gpu):
     lib = _native.load()
-    # find a shape whose split plan needs more than the fixed 32 MiB
-    m, n, k = 960, 2176, 32768  # 255 tiles, K split 8: 64.25 MiB
+    # a shape whose split plan needs more than the fixed 64 MiB
+    m, n, k = 960, 2176, 32768  # 255 tiles of 64 x 128, K split 8: 64.25 MiB
     need = lib.pgs_w8a16_workspace_bytes(m, (ctypes.c_int64 * 1)(n), 1, k, 0)
-    assert need > (32 << 20), need
+    assert need > (64 << 20), need
     rc = _noalloc(lib)(VP(256), VP(256), VP(256), None, VP(256), 1, m, n, k,
                                       VP(torch.cuda.current_stream().cuda_stream))
     assert rc == 1 and b"maximum" in lib.pgs_last_error()
