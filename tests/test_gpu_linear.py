@@ -40,8 +40,10 @@ SHAPES = [
     # K below one 64-column block and K tails on the tiled path; a split-K
     # plan (few tiles, long K) whose last block is partial
     (20, 48, 16), (33, 130, 32), (40, 96, 48), (40, 256, 4112), (70, 2048, 11024),
-    # 33..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also split)
-    (70, 2048, 11008), (128, 2048, 11008), (96, 2560, 2048), (17, 300, 128),
+    # 33..128 tokens, K % 64 == 0: 64-row tiles in four K groups (long K also
+    # split: 4 ways over 64 tiles, 8 ways over 32 or fewer)
+    (70, 2048, 11008), (128, 2048, 11008), (96, 2560, 2048), (17, 300, 128), (64, 2048, 11008),
+    (40, 300, 8192),
     # 33..128 tokens, K <= 2048: one-shot 16-token tiles of 64 / 32 / 16 rows,
     # ragged M and N, a one-chunk K, a K shorter than the tile holds
     (48, 2560, 2048), (40, 1000, 1024), (100, 300, 2048), (128, 64, 64), (33, 4000, 512),
