@@ -1020,7 +1020,8 @@ int launch_once(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 // (o 23.4 vs 24.6 us, q|k|v 29.5 vs 30.5 us at 2048 tokens); at most two
 // work units per CU (o / q|k|v / down_proj at 512 and 1024 tokens): the
 // buffer-load kernel in two K groups per workgroup, or, for a long K over
-// at most one work unit per CU (down_proj at 1024 tokens), four.  Other K:
+// at most one work unit per CU (measured on down_proj at 1024 tokens, which
+// now takes the 128 x 128 split plan, as fast there), four.  Other K:
 // the pointer kernel (SwiGLU: one-step pipeline at the compiler's register
 // budget; single matrices: two-step pipeline at 4 waves per SIMD).
 template <int BM, int NMAT, bool OUT_F32>
@@ -1140,11 +1141,13 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   // 2048] at 256 tokens 165-176 vs 173-184 us; at 320..1376 tiles they are
   // no faster or slower: q|k|v at 2048 tokens 32.5 vs 29.3 us)
   if (nmat == 1 && k % kBK == 0 && p.bn == kBN && m >= 256 && tiles_for(128) >= 2048) p.bm = 128;
-  // a long K (down_proj) above 1024 tokens: 128 x 128 tiles, split K until
-  // 512 workgroups (down_proj [2048, 11008] at 1280 tokens 69.8 vs 79.3 us
-  // and at 1536 78.7 vs 87-90 us with four splits, at 2048 94.5 vs 99-104 us
-  // with two; at 1024 tokens and below within noise of the plans below)
-  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m > 1024;
+  // a long K (down_proj) above 256 tokens: 128 x 128 tiles, split K (up to
+  // 8 ways) until 512 workgroups (down_proj [2048, 11008] at 384 tokens
+  // 33.6-34.1 vs 35.6-36.9 us with eight splits, at 768 52.4-54.1 vs
+  // 57.3-58.8, at 1280 69.8 vs 79.3 and at 1536 78.7 vs 87-90 with four, at
+  // 2048 94.5 vs 99-104 with two; at 512 and 1024 tokens within noise of the
+  // plans below, at 256 no faster)
+  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m > 256;
   if (long128) p.bm = 128;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K
@@ -1154,14 +1157,14 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   p.tiles = p.tiles_m * p.tiles_n;
   p.splits = 1;
   if (long128) {
-    while (p.splits < 4 && static_cast<int64_t>(p.tiles) * p.splits < 512) p.splits *= 2;
+    while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 512) p.splits *= 2;
     return p;
   }
   // fewer than 256 output tiles: split K until about four workgroups per CU,
   // keeping >= 32 K steps per split (>= 8 when there are very few tiles).
   // From 256 tiles on, K groups inside the workgroup beat a split and its
   // reduce launch (down_proj at 1024 tokens 54 vs 58.5-64 us, at 2048: 99
-  // vs 105-110).
+  // vs 105-110; above 256 tokens down_proj now takes the 128 x 128 plan).
   if (can_split && p.tiles < 256) {
     const int min_steps = p.tiles < 128 ? 8 : 32;
     while (p.splits < 8 && static_cast<int64_t>(p.tiles) * p.splits < 1024 && kb / (p.splits * 2) >= min_steps)

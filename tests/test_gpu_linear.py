@@ -292,8 +292,8 @@ def _plan_kernel() -> str:
 
 def test_four_k_group_plan(gpu):
     """The 256-tile, long-K plan (four K groups of four waves per
-    workgroup, launch_k64<64, 128, 1, *, 2, 2, 1, 4>): down_proj's shape at
-    1024 tokens (256 tiles, no split), and a few-tile long-K shape with a
+    workgroup, launch_k64<64, 128, 1, *, 2, 2, 1, 4>): a wide long-K shape at
+    256 tokens (256 tiles, no split), and a few-tile long-K shape with a
     workspace (K split 8 plus the reduce kernel) and without one (the C ABI
     with a NULL workspace: no split)."""
     import ctypes
@@ -301,12 +301,12 @@ def test_four_k_group_plan(gpu):
     from pageserve_amd import _native
 
     kg4 = "BM = 64, BN = 128, NMAT = 1, OUT_F32 = false, WLEAD = 2, XLEAD = 2, OCC = 1, KG = 4"
-    m, n, k = 1024, 2048, 11008
+    m, n, k = 256, 8192, 4160
     qw, q, s, x, _ = _problem(gpu, 7711, m, n, k)
     y = to_np(qw.linear(bf16_gpu(x, gpu)))
     assert kg4 in _plan_kernel() and "splits=1" in _plan_kernel(), _plan_kernel()
     rows = np.concatenate([np.random.default_rng(3).choice(m, 40, replace=False), [0, 63, 64, m - 1]])
-    report(y[rows], O.linear(x[rows], q, s), k, "kg4 m=1024", acc=O.acc_bound(x[rows], q, s))
+    report(y[rows], O.linear(x[rows], q, s), k, "kg4 m=256", acc=O.acc_bound(x[rows], q, s))
 
     m, n, k = 200, 200, 4160
     qw, q, s, x, b = _problem(gpu, 7712, m, n, k, bias=True)
@@ -329,12 +329,12 @@ def test_four_k_group_plan(gpu):
 
 
 def test_long_k_128_tile_plan(gpu):
-    """Above 1024 tokens a long K (more than 64 steps of 64) runs 128 x 128
-    LDS-DMA tiles with the K split until 512 workgroups (launch_dma<128, 128,
-    1, *, 2, 3, 2> plus the reduce kernel): a ragged few-tile shape (four
-    splits) against the full oracle, down_proj's shape at 2048 tokens (two
-    splits) on sampled rows, and the C ABI without a workspace, which keeps
-    the unsplit plan."""
+    """Above 256 tokens a long K (more than 64 steps of 64) runs 128 x 128
+    LDS-DMA tiles with the K split (up to 8 ways) until 512 workgroups
+    (launch_dma<128, 128, 1, *, 2, 3, 2> plus the reduce kernel): a ragged
+    few-tile shape (eight splits) against the full oracle, down_proj's shape
+    at 2048 tokens (two splits) and at 384 (eight) on sampled rows, and the C
+    ABI without a workspace, which keeps the unsplit plan."""
     import ctypes
 
     from pageserve_amd import _native
@@ -345,7 +345,7 @@ def test_long_k_128_tile_plan(gpu):
     xt, bt = bf16_gpu(x, gpu), bf16_gpu(b, gpu)
     y = to_np(qw.linear(xt, bt))
     plan = _plan_kernel()
-    assert t128 in plan and "splits=4" in plan and "gemm_reduce_kernel" in plan, plan
+    assert t128 in plan and "splits=8" in plan and "gemm_reduce_kernel" in plan, plan
     report(y, O.linear(x, q, s, b), k, "128 tile m=1536", acc=O.acc_bound(x, q, s, b))
 
     lib = _native.load()
@@ -360,10 +360,11 @@ def test_long_k_128_tile_plan(gpu):
     assert t128 not in plan and "splits=1" in plan, plan
     report(to_np(out), O.linear(x, q, s, b), k, "no workspace m=1536", acc=O.acc_bound(x, q, s, b))
 
-    m, n, k = 2048, 2048, 11008
-    qw, q, s, x, _ = _problem(gpu, 7731, m, n, k)
-    y = to_np(qw.linear(bf16_gpu(x, gpu)))
-    plan = _plan_kernel()
-    assert t128 in plan and "splits=2" in plan, plan
-    rows = np.concatenate([np.random.default_rng(5).choice(m, 40, replace=False), [0, 127, 128, m - 1]])
-    report(y[rows], O.linear(x[rows], q, s), k, "128 tile m=2048", acc=O.acc_bound(x[rows], q, s))
+    for m, splits, seed in ((2048, 2, 7731), (384, 8, 7732)):
+        n, k = 2048, 11008
+        qw, q, s, x, _ = _problem(gpu, seed, m, n, k)
+        y = to_np(qw.linear(bf16_gpu(x, gpu)))
+        plan = _plan_kernel()
+        assert t128 in plan and f"splits={splits}" in plan, plan
+        rows = np.concatenate([np.random.default_rng(5).choice(m, 40, replace=False), [0, 127, 128, m - 1]])
+        report(y[rows], O.linear(x[rows], q, s), k, f"128 tile m={m}", acc=O.acc_bound(x[rows], q, s))

@@ -78,7 +78,7 @@ def test_noalloc_equals_the_workspace_entry_point(gpu, first, second):
 def test_noalloc_rejects_plans_beyond_its_scratch(gpu):
     lib = _native.load()
     # a shape whose split plan needs more than the fixed 64 MiB
-    m, n, k = 960, 2176, 32768  # 255 tiles of 64 x 128, K split 8: 64.25 MiB
+    m, n, k = 192, 10880, 32768  # 255 tiles of 64 x 128, K split 8: 64.25 MiB
     need = lib.pgs_w8a16_workspace_bytes(m, (ctypes.c_int64 * 1)(n), 1, k, 0)
     assert need > (64 << 20), need
     rc = _noalloc(lib)(VP(256), VP(256), VP(256), None, VP(256), 1, m, n, k,
