@@ -1065,6 +1065,9 @@ int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hip
       if (ga.M > 64) return launch_dma<64, 64, 2, OUT_F32, 3, 4, 3>(x, ga, st);
       return launch_k64<64, 64, 2, OUT_F32, 2, 2, 1, 2>(x, ga, st);
     } else {
+      // single matrices above 128 tokens (short K, few tiles): 32 x 64 tiles
+      // in two K groups
+      if (ga.M > 128) return launch_k64<32, 64, 1, OUT_F32, 2, 2, 2, 2>(x, ga, st);
       // single matrices at 33..128 tokens: 64-row tiles in four K groups
       return plan.bm == 32 ? launch_k64<32, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st)
                            : launch_k64<64, 64, 1, OUT_F32, 2, 2, 1, 4>(x, ga, st);
@@ -1091,6 +1094,19 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   int tiles_n = 0;
   for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
   auto tiles_for = [&](int bm) { return static_cast<int64_t>((m + bm - 1) / bm) * tiles_n; };
+  // a single matrix with a short K above 128 tokens whose 32 x 128 tiles
+  // would number at most 384 (o at 129..768 tokens, q|k|v at 129..608):
+  // 32 x 64 tiles in two K groups, twice the workgroups and an even spread
+  // over the CUs (o at 160 / 256 / 512 / 768 tokens 9.2 / 9.3 / 11.8 / 15.2
+  // vs 13.8 / 11.9 / 12.5 / 17.1 us, q|k|v at 160 / 256 / 512 9.7 / 11.9 /
+  // 15.1 vs 15.2 / 12.6 / 17.3; no faster for q|k|v at 768, 480 tiles, and
+  // slower at 1024 tokens, 512+ tiles: o 19.0 vs 17.2)
+  const bool narrow = !mid && nmat == 1 && k % kBK == 0 && kb <= 64 && tiles_for(32) <= 384;
+  if (narrow) {
+    p.bn = 64;
+    tiles_n = 0;
+    for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
+  }
   if (mid) {
     // a single matrix with K <= 2048: one-shot 16-token tiles of 16, 32 or 64
     // rows, the smallest whose count fills the 256 CUs at most once (o_proj
@@ -1131,7 +1147,7 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
     }
     return p;
   }
-  p.bm = p.bn == 64 ? 128 : m <= 32 ? 32 : 64;
+  p.bm = narrow ? 32 : p.bn == 64 ? 128 : m <= 32 ? 32 : 64;
   // the SwiGLU pair keeps 64-token tiles when its last 128-token tile would be
   // at most half full (160 tokens 27.6 vs 31.6 us, 192: 28.7 vs 30.9, 320:
   // 37.2 vs 41.7, 448: 46.8 vs 47.5; at 384 the 128-token tiles win, 42.7 vs 44.2)

@@ -97,7 +97,7 @@ def test_fp32_output(gpu, m):
     assert r["rel"] < 1e-4
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 24, 32, 48, 64, 96, 128, 512])
+@pytest.mark.parametrize("m", [1, 5, 16, 24, 32, 48, 64, 96, 128, 160, 512, 800])
 def test_grouped_qkv_matches_separate_calls(gpu, m):
     """q/k/v (engine/model.py:168-170) in one launch: each output matches the
     oracle and its single-weight launch within tolerance.  (Not bit for bit:
@@ -368,3 +368,40 @@ def test_long_k_128_tile_plan(gpu):
         assert t128 in plan and f"splits={splits}" in plan, plan
         rows = np.concatenate([np.random.default_rng(5).choice(m, 40, replace=False), [0, 127, 128, m - 1]])
         report(y[rows], O.linear(x[rows], q, s), k, f"128 tile m={m}", acc=O.acc_bound(x[rows], q, s))
+
+
+def test_narrow_tile_plan(gpu):
+    """Short-K single matrices above 128 tokens whose 32 x 128 tiles would
+    number at most 384 run 32 x 64 tiles in two K groups
+    (launch_k64<32, 64, 1, *, 2, 2, 2, 2>): o_proj's shape at 160 tokens (no
+    split) against the full oracle, q|k|v's at 512 on sampled rows, a
+    ragged narrow matrix whose few tiles split K (reduce kernel of 32 x 64
+    tiles) and a ragged K; at 1024 tokens (512 tiles) o_proj keeps the
+    32 x 128 plan."""
+    narrow = "BM = 32, BN = 64, NMAT = 1, OUT_F32 = false, WLEAD = 2, XLEAD = 2, OCC = 2, KG = 2"
+    for m, n, k, seed, split in ((160, 2048, 2048, 7761, False), (200, 100, 2048, 7762, True),
+                                 (300, 1000, 1088, 7763, False)):
+        qw, q, s, x, b = _problem(gpu, seed, m, n, k, bias=n != 2048)
+        y = to_np(qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu) if b is not None else None))
+        plan = _plan_kernel()
+        assert narrow in plan and ("gemm_reduce_kernel" in plan) == split, plan
+        report(y, O.linear(x, q, s, b), k, f"narrow m={m} n={n} k={k}", acc=O.acc_bound(x, q, s, b))
+    m, k = 512, 2048
+    x = activations(7764, m, k)
+    xs = bf16_gpu(x, gpu)
+    ws, qs, ss = [], [], []
+    for j, n in enumerate((2048, 256, 256)):
+        w = weights(7765 + j, n, k)
+        ws.append(Q.QuantizedWeight(torch.from_numpy(w).to(gpu)))
+        q, s = O.quantize_per_channel(w)
+        qs.append(q)
+        ss.append(s)
+    outs = Q.linear_group(xs, ws)
+    assert narrow in _plan_kernel(), _plan_kernel()
+    rows = np.concatenate([np.random.default_rng(9).choice(m, 40, replace=False), [0, 31, 32, m - 1]])
+    for j in range(3):
+        report(to_np(outs[j])[rows], O.linear(x[rows], qs[j], ss[j]), k, f"narrow qkv[{j}]",
+               acc=O.acc_bound(x[rows], qs[j], ss[j]))
+    qw, q, s, x, _ = _problem(gpu, 7768, 1024, 2048, 2048)
+    qw.linear(bf16_gpu(x, gpu))
+    assert narrow not in _plan_kernel() and "BN = 128" in _plan_kernel(), _plan_kernel()
