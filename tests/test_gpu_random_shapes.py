@@ -3,7 +3,8 @@
 The plan picks kernels and tilings by token count m, output rows n and K
 (skinny / paired split / K groups / tile sizes / split K / K-tail pointer
 kernel); hand-picked shapes cover each branch once, this sweep covers their
-combinations: ragged m and n, K a multiple of 16 (half of them of 64), bias
+combinations: ragged m and n, K a multiple of 16 (half of them of 64; up to
+8304, so the long-K split plans are drawn too), bias
 on and off, single linears, q|k|v-style groups, the SwiGLU pair and the
 residual epilogue.  Sizes are capped so the float64 oracle stays fast.
 """
@@ -34,7 +35,7 @@ def _case(i: int):
     band = i % 4
     m = int(rng.integers(1, 17) if band == 0 else rng.integers(17, 129) if band == 1 else rng.integers(129, 700)
             if band == 2 else rng.integers(1, 700))
-    k = 16 * int(rng.integers(1, 260))
+    k = 16 * int(rng.integers(1, 520))  # up to 8304: long-K split plans too
     if i % 2 == 0:
         k = 64 * max(1, k // 64)
     n = int(rng.integers(1, 3200))
