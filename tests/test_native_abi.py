@@ -111,6 +111,38 @@ def test_workspace_query(native_lib):
     assert need(16, [1000], 8192, 1) == 256 * 256 * 8 + 63 * 2 * 2 * 256 * 4
 
 
+def test_tiled_plan_splits(native_lib):
+    """The tiled GEMM planner's K splits, read through the workspace query:
+    512 KiB of pair slots plus tiles x splits x matrices x tile bytes (fp32),
+    or 0 when nothing is split."""
+    def need(m, ns, k, swiglu=0):
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        return native_lib.pgs_w8a16_workspace_bytes(m, arr, len(ns), k, swiglu)
+
+    slots = 256 * 256 * 8
+
+    def split(tiles, splits, bm, bn, nmat=1):
+        return slots + tiles * splits * nmat * bm * bn * 4
+
+    # 33..128 tokens, long K: 64 x 64 tiles split until one workgroup per CU (at most 8)
+    assert need(64, [2048], 11008) == split(32, 8, 64, 64)
+    assert need(40, [300], 8192) == split(5, 8, 64, 64)
+    assert need(128, [2048], 11008) == split(64, 4, 64, 64)
+    # above 256 tokens, long K: 128 x 128 tiles split until 512 workgroups (at most 8)
+    assert need(384, [2048], 11008) == split(48, 8, 128, 128)
+    assert need(512, [2048], 11008) == split(64, 8, 128, 128)
+    assert need(1024, [2048], 11008) == split(128, 4, 128, 128)
+    assert need(1920, [2048], 11008) == split(240, 4, 128, 128)   # 60.5 MiB, the model's largest
+    assert need(2048, [2048], 11008) == split(256, 2, 128, 128)
+    # 129..256 tokens, long K: 64 x 128 tiles, split while under 1024 units
+    assert need(256, [2048], 11008) == split(64, 8, 64, 128)
+    # short K above 128 tokens: 32 x 64 tiles, split only when very few
+    assert need(512, [2048], 2048) == 0 and need(160, [2048, 256, 256], 2048) == 0
+    assert need(200, [100], 2048) == split(14, 4, 32, 64)
+    # the SwiGLU pair at these sizes never splits
+    assert need(128, [11008], 2048, 1) == 0 and need(512, [11008], 2048, 1) == 0
+
+
 def test_rmsnorm_workspace_query(native_lib):
     """The fused-norm calls need room for h = rms_norm(x) (m x k bf16) past
     the linear's own workspace, for the cases that cannot normalise inside

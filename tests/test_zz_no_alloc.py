@@ -46,7 +46,7 @@ def _reference_call(lib, x, qp, sc, b, y, m, n, k, stream):
 # (folded, no scratch); a ragged tiled split then a smaller one; down_proj at
 # 1920 tokens (128 x 128 tiles split four ways, 60.5 MiB, the largest of the
 # model's shapes) then 1280 tokens (the same plan, 40.5 MiB); a narrow short-K
-# matrix (32 x 64 tiles, K split 8) then o_proj at 160 tokens (32 x 64, unsplit)
+# matrix (32 x 64 tiles, K split 4) then o_proj at 160 tokens (32 x 64, unsplit)
 PAIRS = [((200, 2048, 11008), (9, 2048, 2048)), ((5, 2048, 11008), (1, 2048, 11008)),
          ((150, 300, 4160), (40, 200, 4160)), ((1920, 2048, 11008), (1280, 2048, 11008)),
          ((200, 100, 2048), (160, 2048, 2048))]
