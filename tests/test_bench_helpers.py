@@ -37,3 +37,16 @@ def test_kernel_pattern_names_the_launched_instance(plan, kernel, reduce):
 def test_kernel_pattern_rejects_an_unknown_launcher():
     with pytest.raises(ValueError):
         bench.kernel_pattern("int pgs::launch_unknown(void) [A = 1] | grid=1 splits=1")
+
+
+@pytest.mark.parametrize("argv, env", [(["--gpus", "2"], {}), (["--gpus", "8", "--steps", "1"], {}),
+                                       ([], {"WORLD_SIZE": "4"})])
+def test_more_than_one_gpu_exits_with_a_message(argv, env):
+    """`bench.py --gpus N` with N > 1 (or a multi-rank launch) exits before
+    touching a GPU, saying that this path is measured on one GPU."""
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), *argv], capture_output=True, text=True,
+                       env={**os.environ, **env}, timeout=300)
+    assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
