@@ -33,6 +33,7 @@ import argparse
 import json
 import os
 import re
+import statistics
 import sys
 import time
 
@@ -297,15 +298,21 @@ def time_graph(g, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def time_eager(fn, steps, warmup):
+def time_eager(fn, steps, warmup, reps=5):
+    """ms per step of `fn` launched eagerly: the median over `reps` timings of
+    `steps` back-to-back steps each (a rare host pause, such as a full Python
+    garbage collection, lands in one timing instead of the figure)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    runs = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        runs.append((time.perf_counter() - t0) * 1e3 / steps)
+    return statistics.median(runs)
 
 
 def kernel_roofline(layers, launch, bytes_per_launch, flops_per_launch, bound, reps=20):
