@@ -55,7 +55,9 @@ at::Tensor check_x(const at::Tensor& x, int64_t k, const at::Device& dev, const 
   if (x.dim() < 1 || x.size(-1) != k)
     value_error(std::string(what) + ": input has " + std::to_string(x.dim() ? x.size(-1) : 0) +
                 " features, weight expects " + std::to_string(k));
-  return aligned(x.reshape({-1, k}), 16);
+  // (a 2-D input is used as it is: each view op costs a few hundred ns of
+  // host time per call)
+  return aligned(x.dim() == 2 ? x : x.reshape({-1, k}), 16);
 }
 
 std::vector<int64_t> out_shape(const at::Tensor& x, int64_t n) {
@@ -69,7 +71,7 @@ at::Tensor check_bias(const Opt& b, int64_t n, const at::Device& dev, const char
   const at::Tensor& t = *b;
   if (t.device() != dev || t.scalar_type() != at::kBFloat16 || t.numel() != n)
     value_error(std::string(what) + ": bias must be a bf16 [" + std::to_string(n) + "] tensor on " + dev_str(dev));
-  return aligned(t.reshape({n}), 2);
+  return aligned(t.dim() == 1 ? t : t.reshape({n}), 2);
 }
 
 at::Tensor check_norm(const Opt& w, int64_t k, const at::Device& dev, const char* what) {
@@ -117,7 +119,7 @@ std::vector<at::Tensor> linear(const at::Tensor& x, const std::vector<at::Tensor
     bias_keep[i] = check_bias(biases[i], n, dev, what);
     at::Tensor y;
     if (g > 1) {
-      y = flat.narrow(0, off, m * n).view({m, n});
+      y = flat.as_strided({m, n}, {n, 1}, off);  // (a fresh allocation: storage offset 0)
       off += piece(i);
     } else if (out.has_value()) {
       const at::Tensor& o = *out;
@@ -155,7 +157,8 @@ std::vector<at::Tensor> linear(const at::Tensor& x, const std::vector<at::Tensor
   else
     rc = pgs_w8a16_linear_group(ptr(x2), outs, static_cast<int>(g), ydt, m, k, ws, static_cast<size_t>(ws_bytes), st);
   check_rc(rc, "w8a16 linear");
-  for (size_t i = 0; i < g; ++i) ys[i] = ys[i].view(out_shape(x, ns[i]));
+  if (x.dim() != 2)
+    for (size_t i = 0; i < g; ++i) ys[i] = ys[i].view(out_shape(x, ns[i]));
   return ys;
 }
 
@@ -183,7 +186,7 @@ at::Tensor swiglu(const at::Tensor& x, const at::Tensor& qg, const at::Tensor& s
                           static_cast<const int8_t*>(ptr(qu)), static_cast<const float*>(ptr(su)), ptr(act), m, n, k,
                           ws, static_cast<size_t>(ws_bytes), st);
   check_rc(rc, "w8a16 swiglu");
-  return act.view(out_shape(x, n));
+  return x.dim() == 2 ? act : act.view(out_shape(x, n));
 }
 
 }  // namespace
