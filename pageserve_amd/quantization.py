@@ -341,9 +341,10 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
     out: optional contiguous result buffer of the right shape and dtype; it
     may be the residual itself (in place).
     """
-    if out_dtype not in (torch.bfloat16, torch.float32):
+    if out_dtype is not torch.bfloat16 and out_dtype is not torch.float32:
         raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
-    if weight.device.type != "cuda":
+    # (is_cuda rather than .device.type: no torch.device built per call)
+    if not weight.qp.is_cuda:
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
     q, s, n, k, dev = weight._launch_operands()
     ws, ws_bytes = _ws_args(dev, x, k, (n,), False, False)
@@ -504,9 +505,9 @@ def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch
     biases = list(biases) if biases is not None else [None] * len(weights)
     if len(biases) != len(weights):
         raise ValueError("one bias (or None) per weight")
-    if out_dtype not in (torch.bfloat16, torch.float32):
+    if out_dtype is not torch.bfloat16 and out_dtype is not torch.float32:
         raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
-    if weights[0].device.type != "cuda":
+    if not weights[0].qp.is_cuda:
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
     ops = [w._launch_operands() for w in weights]
     _, _, _, k, dev = ops[0]
@@ -534,13 +535,14 @@ def rmsnorm_swiglu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, gate:
 
 
 def _swiglu(x, gate, up, norm_weight, eps) -> torch.Tensor:
-    dev = gate.device
-    if dev.type != "cuda" or up.device != dev:
+    if not gate.qp.is_cuda or not up.qp.is_cuda:
         raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
-    if gate.shape != up.shape:
+    qg, sg, n, k, dev = gate._launch_operands()
+    qu, su, nu, ku, dev_u = up._launch_operands()
+    if dev_u != dev:
+        raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
+    if (n, k) != (nu, ku):
         raise ValueError("swiglu: gate and up weights must have the same shape")
-    qg, sg, n, k, _ = gate._launch_operands()
-    qu, su, _, _, _ = up._launch_operands()
     ws, ws_bytes = _ws_args(dev, x, k, (n,), True, norm_weight is not None)
     return _native.load_host().swiglu(x, qg, sg, qu, su, n, k, norm_weight, eps, ws, ws_bytes)
 
