@@ -162,6 +162,13 @@ std::vector<at::Tensor> linear(const at::Tensor& x, const std::vector<at::Tensor
   return ys;
 }
 
+// One projection (linear and its residual / out forms): the group path
+// without the four one-element lists a Python caller would build.
+at::Tensor linear1(const at::Tensor& x, const at::Tensor& qp, const at::Tensor& scale, const Opt& bias, int64_t n,
+                   int64_t k, bool out_f32, const Opt& residual, const Opt& out, int64_t ws_ptr, int64_t ws_bytes) {
+  return linear(x, {qp}, {scale}, {bias}, {n}, k, out_f32, residual, out, c10::nullopt, 0.0, ws_ptr, ws_bytes)[0];
+}
+
 // gate / up / silu(gate) * up in one launch (norm_w: rms_norm fused in front)
 at::Tensor swiglu(const at::Tensor& x, const at::Tensor& qg, const at::Tensor& sg, const at::Tensor& qu,
                   const at::Tensor& su, int64_t n, int64_t k, const Opt& norm_w, double eps, int64_t ws_ptr,
@@ -195,5 +202,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.doc() = "C++ host path of pageserve_amd's linear entry points (calls the gfx950 C ABI)";
   mod.def("abi_version", &pgs_abi_version);
   mod.def("linear", &linear, "one or more W8A16 projections of the same input");
+  mod.def("linear1", &linear1, "one W8A16 projection");
   mod.def("swiglu", &swiglu, "fused gate/up/silu*up");
 }

@@ -348,8 +348,7 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
     q, s, n, k, dev = weight._launch_operands()
     ws, ws_bytes = _ws_args(dev, x, k, (n,), False, False)
-    return _native.load_host().linear(x, [q], [s], [bias], [n], k, out_dtype is torch.float32, residual, out, None,
-                                      0.0, ws, ws_bytes)[0]
+    return _native.load_host().linear1(x, q, s, bias, n, k, out_dtype is torch.float32, residual, out, ws, ws_bytes)
 
 
 def linear_argmax(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
