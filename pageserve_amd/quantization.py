@@ -769,10 +769,12 @@ class W8A16Weight(torch.Tensor):
             b = args[2] if len(args) > 2 else kwargs.get("bias")
             # metadata is read from the plain QuantizedWeight: a property of the
             # subclass itself would re-enter this handler
+            # (dtypes are singletons, and device indices compare without
+            # building torch.device objects: this runs once per projection)
             if (type(w) is W8A16Weight and type(x) is torch.Tensor
                     and (b is None or type(b) is torch.Tensor)
-                    and w._qw.dtype == torch.bfloat16 and x.dtype == torch.bfloat16
-                    and x.device == w._qw.qp.device):
+                    and w._qw.dtype is torch.bfloat16 and x.dtype is torch.bfloat16
+                    and x.get_device() == w._qw.qp.get_device()):
                 return w._qw.linear(x, b)
         # everything else keeps torch's own behaviour: metadata reads use the
         # wrapper's shape/dtype/device, and compute reaches __torch_dispatch__,
