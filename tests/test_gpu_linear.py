@@ -136,6 +136,32 @@ def test_leading_dims_and_noncontiguous_input(gpu):
     report(to_np(qw.linear(xT)), O.linear(x, q, s), 256, "non-contiguous input", acc=O.acc_bound(x, q, s))
 
 
+def test_leading_dims_through_group_and_swiglu(gpu):
+    """A 3-D input, a 1-D input and a [1, n] bias through the group and
+    SwiGLU calls: outputs keep the input's leading dims and equal the 2-D
+    calls bit for bit (same launch plan), and a group's members are separate
+    tensors with their own storage offsets in one allocation."""
+    k = 256
+    x = activations(7801, 6, k)
+    x2 = bf16_gpu(x, gpu)
+    ws = [Q.QuantizedWeight(torch.from_numpy(weights(7802 + j, n, k)).to(gpu)) for j, n in enumerate((96, 40, 40))]
+    bs = [bf16_gpu(O.round_to_bf16(np.random.default_rng(7810 + j).standard_normal(n).astype(np.float32)), gpu)
+          for j, n in enumerate((96, 40, 40))]
+    flat = Q.linear_group(x2, ws, bs)
+    three = Q.linear_group(x2.reshape(2, 3, k), ws, [bs[0].reshape(1, 96), bs[1], bs[2]])
+    for j, (a, b) in enumerate(zip(flat, three)):
+        assert b.shape == (2, 3, a.shape[1]) and torch.equal(a, b.reshape(a.shape)), j
+        assert a.is_contiguous() and a.data_ptr() % 128 == 0, j
+    assert flat[0].data_ptr() != flat[1].data_ptr() != flat[2].data_ptr()
+    one = Q.linear_group(x2[0], ws, bs)
+    for a, b in zip(flat, one):
+        assert b.shape == (a.shape[1],) and torch.equal(a[0], b)
+    g, u = (Q.QuantizedWeight(torch.from_numpy(weights(7820 + j, 200, k)).to(gpu)) for j in range(2))
+    act = Q.swiglu(x2, g, u)
+    assert torch.equal(Q.swiglu(x2.reshape(2, 3, k), g, u), act.reshape(2, 3, 200))
+    assert torch.equal(Q.swiglu(x2[0], g, u), act[0])
+
+
 def test_full_size_prefill_sampled(gpu):
     """m = 2048 (the largest prefill chunk) on gate_proj's shape: every output
     row and column block checked on a random sample against the oracle."""
