@@ -96,12 +96,12 @@ constexpr int skinny_occ(int nw, int nb, int nmat, int tm) {
   return (tm == 1 && nmat == 2 && nw == 8 && nb == 2) ? 6 : 1;
 }
 
-// LDS of a kernel with xm staged tokens (slots of s chunks; 16 tokens are
-// staged one batch at a time; the fused norm adds its per-wave partial sums);
+// LDS of a kernel with xm staged tokens (slots of s chunks; 8 or 16 tokens
+// are staged one batch at a time; the fused norm adds its per-wave partial sums);
 // at most 160 KiB per workgroup on gfx950.
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int skinny_lds_bytes(int nw, int u, int nb, int nmat, int s, int xm, bool norm) {
-  return (xm > 0 ? nw * (xm == 16 ? 1 : nb) * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
+  return (xm > 0 ? nw * (xm >= 8 ? 1 : nb) * u * s * xm * 9 * 16 : 0) + nw * nmat * 64 * 16 + (norm ? nw * xm * 4 : 0);
 }
 
 // Template parameters:
@@ -262,11 +262,13 @@ __global__ __launch_bounds__(64 * NW, skinny_occ(NW, NB, NMAT, TM)) void skinny_
   // touches its slice.  Slice layout: row (slot chunk, token) of 8 pieces,
   // rows 9 pieces apart, so that the B reads of up to eight rows (XM tokens
   // x 2 chunks) fall on distinct banks (and those of 16 tokens: row r starts
-  // at 144 r bytes, distinct 16-byte bank groups mod 256).  XM = 16 parks one
-  // batch at a time into a slice of one batch (PHASED): all of a wave's
-  // batches would need 9 KiB per wave, too much LDS for the resident
-  // workgroups the weight stream needs.
-  constexpr bool PHASED = XM == 16;
+  // at 144 r bytes, distinct 16-byte bank groups mod 256).  XM = 8 and 16
+  // park one batch at a time into a slice of one batch (PHASED): all of a
+  // wave's batches would need 4.5 / 9 KiB per wave, LDS that the resident
+  // workgroups the weight stream needs do not have (lm_head [151936, 2048]
+  // at 5 / 8 tokens 51.9-54.2 / 56.9-57.9 us phased, 54.9-55.6 / 58.5-59.5
+  // with every batch parked at once).
+  constexpr bool PHASED = XM >= 8;
   constexpr int XP = XM > 0 ? NB * U * S * XM * 8 : 1;
   constexpr int XPASS = (XP + 63) / 64;
   constexpr int XROWS = XM > 0 ? (PHASED ? U * S * XM : NB * U * S * XM) : 1;
