@@ -67,6 +67,7 @@ extern "C" {
 #define PGS_ERR_MISALIGNED 2       /* pointer not aligned to its element size */
 #define PGS_ERR_LAUNCH 3           /* the HIP runtime rejected a kernel launch */
 #define PGS_ERR_NO_DEVICE 4        /* no HIP device, or the stream's device is not a gfx950 */
+#define PGS_ERR_TIMEOUT 5          /* a bounded device-side wait gave up (pgs_w8a16_decode_span_status) */
 
 /* ABI version: bumped whenever a signature below changes. */
 int pgs_abi_version(void);
@@ -336,6 +337,77 @@ int pgs_w8a16_linear_argmax(const void* x, const int8_t* qp, const float* scale,
 
 /* Workspace bytes of pgs_w8a16_linear_argmax (0 for unsupported sizes). */
 size_t pgs_w8a16_argmax_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* One decoder layer's weights after its attention (engine/model.py:184-190). */
+typedef struct pgs_span_weights {
+  const int8_t* qp_o;    const float* s_o;     /* o_proj [hidden, hidden], packed */
+  const void* ln_post;                         /* post_attention_layernorm weight, bf16 [hidden] */
+  const int8_t* qp_gate; const float* s_gate;  /* gate_proj [inter, hidden] */
+  const int8_t* qp_up;   const float* s_up;    /* up_proj [inter, hidden] */
+  const int8_t* qp_down; const float* s_down;  /* down_proj [hidden, inter] */
+} pgs_span_weights;
+
+/* The next layer's part before its attention (engine/model.py:165-173). */
+typedef struct pgs_span_next {
+  const void* ln_in;                 /* input_layernorm weight, bf16 [hidden] */
+  pgs_linear_out q, k, v;            /* q/k/v projections: weight, scale, bias (or NULL), output [m, n] bf16 */
+  const void* cos; const void* sin;  /* bf16 [m, head_dim] rows of the RoPE tables (applied to q and k), or NULL */
+  int64_t head_dim;
+} pgs_span_next;
+
+/*
+ * Replaces everything one decode step runs between two attention calls --
+ * engine/model.py:184-190 of layer l, then :165-173 of layer l + 1 -- with
+ * one launch:
+ *   x1 = residual + o_proj(attn)          (pgs_w8a16_linear_residual)
+ *   h  = rms_norm(x1, ln_post, eps)       (pgs_rmsnorm)
+ *   a  = silu(gate(h)) * up(h)            (pgs_w8a16_swiglu)
+ *   x_out = x1 + down(a)                  (pgs_w8a16_linear_residual)
+ *   h' = rms_norm(x_out, next->ln_in, eps)
+ *   q, k, v = projections of h' (+ bias); RoPE of q and k with cos/sin
+ * each with the rounding of the entry point named beside it (results equal
+ * those of the chain of those entry points up to the order of the fp32 sums).
+ * next = NULL: the last layer (no q/k/v).  The weights stream from HBM once,
+ * in one persistent launch of one workgroup per CU whose stages meet through
+ * tagged exchanges in the workspace, so the device must not run other work
+ * meanwhile.  Compiled configurations: pgs_w8a16_decode_span_supported().
+ * attn, residual, x_out: bf16 [m, hidden]; x_out may not alias residual.
+ * workspace: pgs_w8a16_decode_span_workspace_bytes() bytes, 256-byte
+ * aligned, zero-filled before its first use; calls sharing it must be
+ * stream-ordered.  The waits inside the launch are bounded: a launch that
+ * gives up (a workgroup that never ran, another kernel occupying CUs) leaves
+ * an error word in the workspace and returns; later launches on that
+ * workspace then do nothing until pgs_w8a16_decode_span_status() clears it.
+ * No counterpart in the reference (its forward_step runs these as separate
+ * torch calls).
+ */
+int pgs_w8a16_decode_span(const void* attn, const void* residual, void* x_out,
+                          const pgs_span_weights* w, const pgs_span_next* next,
+                          float eps, int64_t m, int64_t hidden, int64_t inter,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of pgs_w8a16_decode_span (0 for unsupported sizes). */
+size_t pgs_w8a16_decode_span_workspace_bytes(int64_t m, int64_t hidden, int64_t inter);
+
+/* 1 if pgs_w8a16_decode_span has a compiled configuration for these sizes. */
+int pgs_w8a16_decode_span_supported(int64_t m, int64_t hidden, int64_t inter,
+                                    int64_t nq, int64_t nkv, int64_t head_dim);
+
+/*
+ * Synchronises `stream` and reads the workspace's error word: PGS_OK, or
+ * PGS_ERR_TIMEOUT if a launch gave up since the workspace was cleared; with
+ * reset != 0 the workspace header and exchange buffers are then zero-filled
+ * (a kernel on `stream`) so the next launch can run.
+ */
+int pgs_w8a16_decode_span_status(void* workspace, int reset, void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: the number of polls after
+ * which a decode span launch gives up (0 = the default), and force_giveup
+ * != 0 makes every launch wait for a tag that no workgroup writes, so that
+ * the give-up path runs.  Process-wide; affects later launches.
+ */
+int pgs_w8a16_decode_span_test_hooks(int spin_limit, int force_giveup);
 
 #ifdef __cplusplus
 }

@@ -23,11 +23,16 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 8
+ABI_VERSION = 9
+ERR_TIMEOUT = 5
 
 
 class NativeLibraryError(RuntimeError):
     """The gfx950 library is missing, stale or failed a call."""
+
+
+class DeviceWaitTimeout(NativeLibraryError):
+    """A bounded wait inside a persistent launch gave up (PGS_ERR_TIMEOUT)."""
 
 
 class LinearOut(ctypes.Structure):
@@ -39,6 +44,29 @@ class LinearOut(ctypes.Structure):
         ("bias", ctypes.c_void_p),
         ("y", ctypes.c_void_p),
         ("n", ctypes.c_int64),
+    ]
+
+
+class SpanWeights(ctypes.Structure):
+    """``pgs_span_weights`` of include/pageserve_amd.h."""
+
+    _fields_ = [
+        ("qp_o", ctypes.c_void_p), ("s_o", ctypes.c_void_p),
+        ("ln_post", ctypes.c_void_p),
+        ("qp_gate", ctypes.c_void_p), ("s_gate", ctypes.c_void_p),
+        ("qp_up", ctypes.c_void_p), ("s_up", ctypes.c_void_p),
+        ("qp_down", ctypes.c_void_p), ("s_down", ctypes.c_void_p),
+    ]
+
+
+class SpanNext(ctypes.Structure):
+    """``pgs_span_next`` of include/pageserve_amd.h."""
+
+    _fields_ = [
+        ("ln_in", ctypes.c_void_p),
+        ("q", LinearOut), ("k", LinearOut), ("v", LinearOut),
+        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("head_dim", ctypes.c_int64),
     ]
 
 
@@ -76,6 +104,12 @@ SIGNATURES = {
     "pgs_w8a16_rmsnorm_workspace_bytes": (_SZ, [_I64, ctypes.POINTER(_I64), _INT, _I64, _INT]),
     "pgs_w8a16_linear_argmax": (_INT, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "pgs_w8a16_argmax_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "pgs_w8a16_decode_span": (_INT, [_VP, _VP, _VP, ctypes.POINTER(SpanWeights), ctypes.POINTER(SpanNext),
+                                     ctypes.c_float, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "pgs_w8a16_decode_span_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "pgs_w8a16_decode_span_supported": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "pgs_w8a16_decode_span_status": (_INT, [_VP, _INT, _VP]),
+    "pgs_w8a16_decode_span_test_hooks": (_INT, [_INT, _INT]),
 }
 
 _lock = threading.Lock()
@@ -181,5 +215,5 @@ def check(rc: int, what: str) -> None:
     lib = load()
     detail = lib.pgs_last_error().decode(errors="replace")
     kind = lib.pgs_error_string(rc).decode(errors="replace")
-    exc = ValueError if rc in (1, 2) else NativeLibraryError
+    exc = ValueError if rc in (1, 2) else DeviceWaitTimeout if rc == ERR_TIMEOUT else NativeLibraryError
     raise exc(f"{what}: {kind}: {detail}")

@@ -85,7 +85,7 @@ void note_launch(const char* kernel, long long grid, int splits, const char* sec
 
 extern "C" {
 
-int pgs_abi_version(void) { return 8; }
+int pgs_abi_version(void) { return 9; }
 
 const char* pgs_error_string(int code) {
   switch (code) {
@@ -94,6 +94,7 @@ const char* pgs_error_string(int code) {
     case PGS_ERR_MISALIGNED: return "misaligned pointer";
     case PGS_ERR_LAUNCH: return "kernel launch failed";
     case PGS_ERR_NO_DEVICE: return "no usable gfx950 device";
+    case PGS_ERR_TIMEOUT: return "a bounded device-side wait gave up";
     default: return "unknown error";
   }
 }

@@ -1,0 +1,856 @@
+// One launch per attention gap of a decode step: everything a decoder layer
+// runs between two attention calls (engine/model.py:184-190, then the next
+// layer's :165-173):
+//
+//   x1  = residual + o_proj(attn)                       (:184)
+//   h   = rms_norm(x1, post_attention_layernorm)        (:187)
+//   act = silu(gate_proj(h)) * up_proj(h)               (:188-189)
+//   x2  = x1 + down_proj(act)                           (:190)
+//   h'  = rms_norm(x2, next input_layernorm)            (:166)
+//   q, k, v = q|k|v_proj(h') (+ bias), RoPE of q and k  (:168-173)
+//
+// The four linears depend on each other through whole vectors (every output
+// of one feeds every output of the next), so separate launches leave the
+// HBM weight stream idle at each boundary: the launch gap, the first bytes'
+// latency and the slowest workgroup's tail, four times per layer.  Here one
+// persistent workgroup per CU streams its share of all four weight matrices
+// through a ring of loads that keeps running across the dependencies, and
+// the dependencies are met by exchanges through memory inside the launch.
+//
+// Roles inside a workgroup of 16 waves:
+//  * 15 streaming waves own a fixed list of 1 KiB weight loads (packed tile
+//    layout, folded 8-row units: two 64-k chunks per MFMA, as the skinny
+//    kernel's folded halves) over the four stages.  A wave keeps span_ring
+//    loads in flight, issuing the next load as soon as one is consumed, so
+//    the next stage's weights arrive while the current dependency is being
+//    met.  Its waits are on its own loads and on workgroup barriers only:
+//    it never waits for memory that another workgroup writes, whose loads
+//    would queue behind its weight loads (vector memory returns in order).
+//  * 1 control wave holds no weight loads.  It sums the streaming waves'
+//    partial tiles (fixed order), runs each stage's epilogue, publishes the
+//    workgroup's outputs to an exchange buffer and gathers every
+//    workgroup's outputs for the next stage.
+//
+// The exchange carries the data with its own validity: each 32-bit word is a
+// bf16 value in the low half and a 16-bit tag in the high half, written and
+// read at agent scope (sc1: coherent across the XCDs' L2 caches), so a
+// reader needs no flag, counter or fence -- a word is valid once its tag is
+// the launch's tag.  The tag comes from an epoch word in the workspace that
+// workgroup 0 advances once every workgroup has read it (after the first
+// exchange, which every workgroup contributes to), so a HIP graph that
+// replays the launch gets a new tag every time.  Every word of the exchange
+// buffers is rewritten by every launch, so a stale word holds the previous
+// launch's tag, never the current one.
+//
+// Every wait is bounded: a gather that has not seen every tag after
+// spin_limit polls writes an error word into the workspace, and the whole
+// workgroup returns normally at its next barrier.  A launch that finds the
+// error word set returns at once; the host reads the word
+// (pgs_w8a16_decode_span_status) and must clear the workspace before its
+// next use.
+//
+// Residency: the grid is one workgroup per CU (a launch of exactly the
+// device's CU count, checked against the occupancy query) and nothing else
+// may run on the device meanwhile, or a gather waits for a workgroup that
+// cannot start; the bound above then ends the launch with an error.
+#include <atomic>
+#include <type_traits>
+
+#include "pgs_linear.h"
+
+// Phase marks for tuning builds (a timing harness defines PGS_SPAN_MARK to
+// record a timestamp per workgroup and phase); nothing by default.
+#ifndef PGS_SPAN_MARK
+#define PGS_SPAN_MARK(i)
+#endif
+
+namespace pgs {
+namespace {
+
+constexpr int kSpanG = 256;                       // workgroups: one per CU
+constexpr int kSpanSW = 15;                       // streaming waves per workgroup
+constexpr int kSpanThreads = 64 * (kSpanSW + 1);  // + one control wave
+// Weight loads in flight per streaming wave.  Deeper is not better: a CU's
+// vector memory requests are served in order, so every load queued when
+// the control wave polls an exchange delays the poll; the ring only has to
+// cover the memory latency at the CU's share of the bandwidth.
+constexpr int kSpanRingDefault = 4;
+constexpr int kSlot = 128;                        // exchange bytes per 8-row unit (8 rows x <= 4 tokens x 4 B)
+constexpr int kHeader = 256;                      // workspace header: [0] epoch, [1] error word
+constexpr int kSC1 = 16;                          // cache policy: sc1 (agent scope)
+constexpr int kMinLds = 84 * 1024;                // > half the CU's LDS: one workgroup per CU
+
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// The model dimensions a kernel instance is compiled for.
+template <int H_, int I_, int NQ_, int NKV_, int HD_>
+struct Dims {
+  static constexpr int H = H_, I = I_, NQ = NQ_, NKV = NKV_, HD = HD_;
+  static_assert(H % 128 == 0 && I % 128 == 0, "K ranges are whole 128-k fold slots");
+  static_assert(NQ % HD == 0 && NKV % HD == 0 && HD % 16 == 0, "whole heads of whole 8-row unit pairs");
+};
+using Qwen25_3B = Dims<2048, 11008, 2048, 256, 128>;
+
+// Stage geometry.  Stage 0: o_proj, 1: gate|up, 2: down_proj, 3: q|k|v.
+// A unit is 8 rows of one matrix over its whole K (half of a 16-row tile,
+// folded: two 64-k chunks per MFMA); an item is one 128-k slot of a unit
+// (one 1 KiB load per matrix); the items of a workgroup's units are dealt to
+// the streaming waves in contiguous runs of P.
+template <class DM, int M>
+struct Geo {
+  static constexpr int H = DM::H, I = DM::I;
+  // q and k heads in unit pairs (rows i and i + HD/2 of a head, for RoPE), v
+  // units alone
+  static constexpr int kQP = DM::NQ / 16, kKP = DM::NKV / 16, kVS = DM::NKV / 8;
+  static constexpr int units(int s) { return s == 1 ? I / 8 : s == 3 ? (DM::NQ + 2 * DM::NKV) / 8 : H / 8; }
+  static constexpr int U(int s) { return s == 3 ? 2 : cdiv(units(s), kSpanG); }
+  static constexpr int ipu(int s) { return (s == 2 ? I : H) / 128; }
+  static constexpr int kdim(int s) { return s == 2 ? I : H; }
+  static constexpr int nl(int s) { return s == 1 ? 2 : 1; }
+  static constexpr int P(int s) { return cdiv(U(s) * ipu(s), kSpanSW); }
+  static constexpr int lb(int s) {
+    int b = 0;
+    for (int i = 0; i < s; ++i) b += P(i) * nl(i);
+    return b;
+  }
+  static constexpr int kLoads = lb(4);
+  static constexpr int stage_of(int li) { return li < lb(1) ? 0 : li < lb(2) ? 1 : li < lb(3) ? 2 : 3; }
+  // B operand rows in LDS: [M][K + 64] bf16 (the pad staggers the tokens)
+  static constexpr int ks(int s) { return kdim(s) + 64; }
+  static constexpr int kBBytes = M * (cmax(H, I) + 64) * 2;
+  // gathered exchange words, compact [unit][2M pieces of 16 B]
+  static constexpr int kTagBytes = cmax(H, I) * 4 * M;
+  static constexpr int kPartFloats = kSpanSW * 2 * 2 * 8 * M;
+  static constexpr int kOffB = 0;
+  static constexpr int kOffTag = kOffB + kBBytes;
+  static constexpr int kOffLn = kOffTag + kTagBytes;  // two norm weights [H] bf16
+  static constexpr int kOffPart = kOffLn + 2 * H * 2;
+  static constexpr int kOffSsq = kOffPart + kPartFloats * 4;
+  static constexpr int kOffFlag = kOffSsq + 16 * M * 4;
+  static constexpr int kLds = cmax(kOffFlag + 16, kMinLds);
+  static_assert(kLds <= 160 * 1024, "LDS of one workgroup");
+  static_assert(P(0) <= ipu(0) && P(1) <= ipu(1) && P(2) <= ipu(2) && P(3) <= ipu(3),
+                "a wave's run touches at most two units");
+  static_assert(8 * M * 4 <= kSlot, "a unit's outputs fit its exchange slot");
+};
+
+// Kernel arguments (device pointers; see pgs_w8a16_decode_span).
+struct SpanParams {
+  const uint16_t* attn;
+  const uint16_t* resid;
+  uint16_t* x_out;
+  const int8_t* qo;
+  const float* so;
+  const uint16_t* ln_post;
+  const int8_t* qg;
+  const float* sg;
+  const int8_t* qu;
+  const float* su;
+  const int8_t* qd;
+  const float* sd;
+  const uint16_t* ln_next;  // null: no q|k|v stage (last layer)
+  const int8_t* qkv[3];
+  const float* sqkv[3];
+  const uint16_t* bqkv[3];
+  uint16_t* yqkv[3];
+  const uint16_t* cos;  // null: no RoPE
+  const uint16_t* sin;
+  uint32_t* ws;
+  float eps;
+  int spin_limit;
+  int force_giveup;
+};
+
+// Where a unit's weights are: its 16-row block row (whole K) and the byte
+// offset of its 8-row half inside a block.
+struct URef {
+  const int8_t* blk;
+  int half;
+  bool ok;
+};
+
+// Unit lu (0 .. U-1) of workgroup wg in stage S.  q|k|v: workgroups
+// [0, kQP) take a q pair (8 rows of a head's first half and their partners
+// HD/2 rows on), [kQP, kQP + kKP) a k pair, then one v unit each.
+template <class DM, int M, int S>
+__device__ __forceinline__ URef unit_ref(const SpanParams& p, int wg, int lu, int mat, int* member, int* row0) {
+  using G = Geo<DM, M>;
+  URef u{nullptr, 0, false};
+  if constexpr (S == 3) {
+    constexpr int HO = DM::HD / 16, HU = DM::HD / 8;
+    int mem = 0, unit = 0;
+    bool ok = p.ln_next != nullptr;
+    if (wg < G::kQP) {
+      unit = (wg / HO) * HU + wg % HO + lu * HO;
+    } else if (wg < G::kQP + G::kKP) {
+      const int pr = wg - G::kQP;
+      mem = 1;
+      unit = (pr / HO) * HU + pr % HO + lu * HO;
+    } else if (wg < G::kQP + G::kKP + G::kVS && lu == 0) {
+      mem = 2;
+      unit = wg - G::kQP - G::kKP;
+    } else {
+      ok = false;
+    }
+    const int8_t* q = pick_early(p.qkv, mem);
+    if (member) *member = mem;
+    if (row0) *row0 = unit * 8;
+    u.blk = q + static_cast<int64_t>(unit >> 1) * (DM::H / 64) * 1024;
+    u.half = unit & 1;
+    u.ok = ok && q != nullptr;
+  } else {
+    const int g = wg + kSpanG * lu;
+    const int8_t* q = S == 0 ? p.qo : S == 2 ? p.qd : (mat ? p.qu : p.qg);
+    constexpr int kb = G::kdim(S) / 64;
+    if (row0) *row0 = g * 8;
+    u.blk = q + static_cast<int64_t>(g >> 1) * kb * 1024;
+    u.half = g & 1;
+    u.ok = g < G::units(S);
+  }
+  return u;
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, kSC1);
+}
+
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// Gathers every unit's tagged outputs of one exchange buffer into LDS
+// (compact [unit][2M pieces]) by LDS DMA, until every word carries `want`
+// (control wave only).  Each poll fetches only the pieces whose tags were
+// stale in the previous one (each lane keeps a bitmask of its pieces): a
+// CU's vector memory requests are served in order, so every byte a poll
+// fetches delays it and whatever follows it.  Returns false after
+// spin_limit polls.
+template <int M, int NUNITS>
+__device__ __forceinline__ bool gather(const uint32_t* xbuf, unsigned char* lds_tag, uint32_t want, int spin_limit) {
+  constexpr int NP = NUNITS * 2 * M, NI = cdiv(NP, 64), NW = cdiv(NI, 32);
+  const int lane = threadIdx.x & 63;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(xbuf, static_cast<int64_t>(NUNITS) * kSlot);
+  uint32_t stale[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) stale[w] = 0xffffffffu;
+  for (int spin = 0;; ++spin) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int pc = lane + 64 * i;
+      if (stale[i / 32] & (1u << (i % 32))) {
+        const int off = pc < NP ? (pc / (2 * M)) * kSlot + (pc % (2 * M)) * 16 : 0x7ffffff0;
+        dma16(r, lds_tag + i * 1024, off);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    bool left = false;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int pc = lane + 64 * i;
+      if (stale[i / 32] & (1u << (i % 32))) {
+        bool ok = pc >= NP;
+        if (!ok) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(lds_tag + pc * 16);
+          ok = (v[0] >> 16) == want && (v[1] >> 16) == want && (v[2] >> 16) == want && (v[3] >> 16) == want;
+        }
+        if (ok) stale[i / 32] &= ~(1u << (i % 32));
+        left |= !ok;
+      }
+    }
+    if (!__any(left)) return true;
+    if (spin >= spin_limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Word index of (token t, row n) in the compact gathered layout.
+template <int M>
+__device__ __forceinline__ int tag_word(int t, int n) {
+  return (n >> 3) * (8 * M) + t * 8 + (n & 7);
+}
+
+// All waves: B operand of the next stage from the gathered words.  NORM:
+// rms_norm (engine/model.py:29-34) with the norm weight in LDS:
+// r = 1 / sqrt(mean(x^2) + eps), h = bf16(w * bf16(x * r)); the sum of
+// squares in a fixed order (per thread, then a wave butterfly, then the 16
+// waves in order).  Two barriers when NORM (the wave sums meet in LDS).
+template <int M, int K, int KS, bool NORM>
+__device__ __forceinline__ void stage_b(unsigned char* smem, int off_tag, int off_b, int off_ln, int off_ssq,
+                                        float eps) {
+  constexpr int E = M * K / 2;  // dwords (bf16 pairs)
+  constexpr int NE = cdiv(E, kSpanThreads);
+  const uint32_t* tw = reinterpret_cast<const uint32_t*>(smem + off_tag);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t w0[NE], w1[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = tid + kSpanThreads * i;
+    const int t = e / (K / 2), n = 2 * (e % (K / 2));
+    if (e < E) {
+      const int wi = tag_word<M>(t, n);
+      w0[i] = tw[wi];
+      w1[i] = tw[wi + 1];
+    } else {
+      w0[i] = w1[i] = 0;
+    }
+  }
+  float r[M];
+  if constexpr (NORM) {
+    float ss[M];
+#pragma unroll
+    for (int t = 0; t < M; ++t) ss[t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = tid + kSpanThreads * i;
+      const int t = e / (K / 2);
+      const float a = bf16_bits_to_f32(w0[i] & 0xffffu), b = bf16_bits_to_f32(w1[i] & 0xffffu);
+#pragma unroll
+      for (int tt = 0; tt < M; ++tt)
+        if (e < E && t == tt) {
+          ss[tt] += a * a;
+          ss[tt] += b * b;
+        }
+    }
+    float* ssq = reinterpret_cast<float*>(smem + off_ssq);
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      float v = ss[t];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+      if (lane == 0) ssq[wave * M + t] = v;
+    }
+    barrier_lds();
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) tot += ssq[w * M + t];
+      r[t] = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+    }
+  }
+  const uint16_t* ln = reinterpret_cast<const uint16_t*>(smem + off_ln);
+  uint32_t* bdst = reinterpret_cast<uint32_t*>(smem + off_b);
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = tid + kSpanThreads * i;
+    if (e >= E) continue;
+    const int t = e / (K / 2), n = 2 * (e % (K / 2));
+    uint32_t out;
+    if constexpr (NORM) {
+      float rt = r[0];
+#pragma unroll
+      for (int tt = 1; tt < M; ++tt) rt = t == tt ? r[tt] : rt;
+      const float a = bf16_bits_to_f32(w0[i] & 0xffffu), b = bf16_bits_to_f32(w1[i] & 0xffffu);
+      out = pack_bf16x2(bf16_bits_to_f32(ln[n]) * bf16r(a * rt), bf16_bits_to_f32(ln[n + 1]) * bf16r(b * rt));
+    } else {
+      out = (w0[i] & 0xffffu) | (w1[i] << 16);
+    }
+    bdst[(t * KS + n) >> 1] = out;
+  }
+}
+
+template <class DM, int M, int RING = kSpanRingDefault>
+__global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
+  using G = Geo<DM, M>;
+  constexpr int H = DM::H, I = DM::I;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[G::kLds];
+  const int wg = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool control = wave == kSpanSW;
+  const bool has_qkv = p.ln_next != nullptr;
+  int* flag = reinterpret_cast<int*>(smem + G::kOffFlag);  // [0] abort
+  float* part = reinterpret_cast<float*>(smem + G::kOffPart);
+  unsigned char* ltag = smem + G::kOffTag;
+  uint32_t* const ws = p.ws;
+  uint32_t* const x1x = ws + kHeader / 4;
+  uint32_t* const actx = x1x + (H / 8) * (kSlot / 4);
+  uint32_t* const x2x = actx + (I / 8) * (kSlot / 4);
+
+  // ---- streaming-wave state -------------------------------------------
+  const int lrow = lane & 15, kgrp = lane >> 4;
+  // A operand: this lane's 16 bytes of a fold slot (rows of the unit's half
+  // in chunk 2j + lrow / 8); B operand: column lrow = token lrow % M of chunk
+  // 2j + lrow / M (columns past 2M read token 0, unused)
+  const int avoff = (lrow >> 3) * 1024 + ((lrow & 7) + 16 * kgrp) * 16;
+  const int btok = lrow < 2 * M ? lrow % M : 0, bsub = lrow < 2 * M ? lrow / M : 0;
+  constexpr int kSpanRing = RING;
+  u32x4 ring[kSpanRing];
+  f32x4 acc[2][2];
+
+  auto issue = [&](auto LI) {
+    constexpr int li = decltype(LI)::value;
+    if constexpr (li < G::kLoads) {
+      constexpr int S = G::stage_of(li);
+      constexpr int it = (li - G::lb(S)) / G::nl(S), mat = (li - G::lb(S)) % G::nl(S);
+      const int item = G::P(S) * wave + it;
+      const int lu = item / G::ipu(S), slot = item - lu * G::ipu(S);
+      const URef u = unit_ref<DM, M, S>(p, wg, lu, mat, nullptr, nullptr);
+      const bool ok = u.ok && item < G::U(S) * G::ipu(S);
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(ok ? u.blk : p.qo, ok ? (G::kdim(S) / 64) * 1024 : 0);
+      ring[li % kSpanRing] = __builtin_amdgcn_raw_buffer_load_b128(r, avoff, uniform(slot * 2048 + u.half * 128), kLoadNT);
+    }
+  };
+  auto zero_acc = [&] {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) acc[a][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  // the items of stage S: MFMAs on the ring's loads, each consumed load
+  // replaced by the one kSpanRing further down the list
+  auto run_stage = [&](auto SI) {
+    constexpr int S = decltype(SI)::value;
+    const int first = G::P(S) * wave;
+    const int lu0 = first / G::ipu(S);
+    const unsigned char* bbase = smem + G::kOffB + (btok * G::ks(S) + bsub * 64 + 16 * kgrp) * 2;
+    static_for<0, G::P(S)>([&](auto IT) {
+      constexpr int it = decltype(IT)::value;
+      const int item = first + it;
+      const int lu = item / G::ipu(S), slot = item - lu * G::ipu(S);
+      const bool ok = unit_ref<DM, M, S>(p, wg, lu, 0, nullptr, nullptr).ok && item < G::U(S) * G::ipu(S);
+      if (ok) {
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(bbase + slot * 256);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(bbase + slot * 256 + 16);
+        const bf16x8 x0 = __builtin_bit_cast(bf16x8, b0), x1 = __builtin_bit_cast(bf16x8, b1);
+        const bool second = lu != lu0;
+        static_for<0, G::nl(S)>([&](auto MT) {
+          constexpr int mat = decltype(MT)::value;
+          const u32x4 w = ring[(G::lb(S) + it * G::nl(S) + mat) % kSpanRing];
+          const bf16x8 a0 = i8x8_to_bf16x8(w[0], w[1]), a1 = i8x8_to_bf16x8(w[2], w[3]);
+          if (second) {
+            acc[1][mat] = mfma16x16x32(a0, x0, acc[1][mat]);
+            acc[1][mat] = mfma16x16x32(a1, x1, acc[1][mat]);
+          } else {
+            acc[0][mat] = mfma16x16x32(a0, x0, acc[0][mat]);
+            acc[0][mat] = mfma16x16x32(a1, x1, acc[0][mat]);
+          }
+        });
+      }
+      static_for<0, G::nl(S)>([&](auto MT) {
+        issue(std::integral_constant<int, G::lb(S) + it * G::nl(S) + decltype(MT)::value + kSpanRing>{});
+      });
+    });
+    // partial tiles: output (token t, row r) of a folded unit is
+    // C[r][t] + C[r + 8][t + M]; C[i][j] sits in lane 16 (i / 4) + j,
+    // register i % 4
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int mat = 0; mat < G::nl(S); ++mat) {
+        f32x4 v = acc[a][mat];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += __shfl_down(v[i], 32 + M);
+        const int t = lane & 15;
+        if (lane < 32 && t < M) {
+          float* dst = part + ((wave * 2 + a) * 2 + mat) * (8 * M) + t * 8 + (lane >> 4) * 4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[i] = v[i];
+        }
+      }
+    zero_acc();
+  };
+
+  // ---- control-wave state -------------------------------------------------
+  // outputs per lane: o / down: (t, r) = (idx / 8, idx % 8) of this
+  // workgroup's unit; gate|up: idx = (lu, t, r); q|k|v: (t, r) of the unit
+  // (pair)
+  constexpr int NO = cdiv(8 * M, 64), NG = cdiv(G::U(1) * 8 * M, 64);
+  static_assert(NO == 1, "one o/down output per control lane");
+  uint32_t tag = 0;
+  float so_r = 0.f, sd_r = 0.f, res_r = 0.f, x1_r = 0.f;
+  float sg_r[NG], su_r[NG];
+  float sq_r[2], bq_r[2], cs_r[4];
+  int qmem = 0, qrow[2] = {0, 0};
+
+  // reduces unit lu's partial tiles of stage S for output (t, r), matrix mat
+  auto reduce = [&](auto SI, int lu, int mat, int t, int r) {
+    constexpr int S = decltype(SI)::value;
+    constexpr int P = G::P(S), IPU = G::ipu(S);
+    const int s_lo = lu * IPU / P, s_hi = cmin(kSpanSW - 1, ((lu + 1) * IPU - 1) / P);
+    float v = 0.f;
+    for (int s = s_lo; s <= s_hi; ++s) {
+      const int a = lu - (P * s) / IPU;
+      v += part[((s * 2 + a) * 2 + mat) * (8 * M) + t * 8 + r];
+    }
+    return v;
+  };
+  auto giveup = [&] {
+    if (lane == 0) {
+      st_agent(ws + 1, 1u);
+      flag[0] = 1;
+    }
+  };
+  auto abort_now = [&] {
+    if (flag[0]) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      return true;
+    }
+    return false;
+  };
+
+  PGS_SPAN_MARK(0);
+  // ================= prologue =================
+  // The control wave's loads go first: they are served before any weight
+  // load of this CU (a barrier orders the streaming waves' first loads
+  // after them), so the launch's operands are not queued behind the ring.
+  constexpr int PC = M * H / 8, NA = cdiv(PC, 64), NL = cdiv(H / 8, 64);
+  u32x4 attn_v[NA], lnp_v[NL], lnn_v[NL];
+  uint32_t ep = 0, err = 0;
+  if (control) {
+    ep = ld_agent(ws);
+    err = ld_agent(ws + 1);
+    // o_proj's B operand (the attention output) and the two norm weights
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int pc = cmin(lane + 64 * i, PC - 1);
+      attn_v[i] = ld16(p.attn + static_cast<int64_t>(pc / (H / 8)) * H + 8 * (pc % (H / 8)));
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int pc = cmin(lane + 64 * i, H / 8 - 1);
+      lnp_v[i] = ld16(p.ln_post + 8 * pc);
+      lnn_v[i] = ld16((has_qkv ? p.ln_next : p.ln_post) + 8 * pc);
+    }
+    // epilogue operands
+    {
+      const int t = cmin(lane / 8, M - 1), r = lane % 8, row = cmin(8 * wg + r, H - 1);
+      so_r = p.so[row];
+      sd_r = p.sd[row];
+      res_r = bf16_bits_to_f32(p.resid[static_cast<int64_t>(t) * H + row]);
+    }
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int idx = lane + 64 * i;
+      const int lu = idx / (8 * M), r = idx % 8;
+      const int g = cmin(wg + kSpanG * lu, I / 8 - 1);
+      sg_r[i] = p.sg[8 * g + r];
+      su_r[i] = p.su[8 * g + r];
+    }
+    if (has_qkv) {
+      const int t = cmin(lane / 8, M - 1), r = lane % 8;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int mem = 0, row0 = 0;
+        const URef u = unit_ref<DM, M, 3>(p, wg, j, 0, &mem, &row0);
+        sq_r[j] = bq_r[j] = 0.f;
+        qrow[j] = row0 + r;
+        if (j == 0) qmem = mem;
+        if (u.ok) {
+          sq_r[j] = pick_early(p.sqkv, mem)[row0 + r];
+          const uint16_t* b = pick_early(p.bqkv, mem);
+          if (b) bq_r[j] = bf16_bits_to_f32(b[row0 + r]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cs_r[c] = 0.f;
+      if (p.cos && qmem < 2) {
+        constexpr int HD = DM::HD;
+        const int i = qrow[0] % HD;  // < HD / 2: the pair's first row
+        const int64_t base = static_cast<int64_t>(t) * HD;
+        cs_r[0] = bf16_bits_to_f32(p.cos[base + i]);
+        cs_r[1] = bf16_bits_to_f32(p.sin[base + i]);
+        cs_r[2] = bf16_bits_to_f32(p.cos[base + i + HD / 2]);
+        cs_r[3] = bf16_bits_to_f32(p.sin[base + i + HD / 2]);
+      }
+    }
+  }
+  barrier_lds();
+  if (!control) {
+    zero_acc();
+    static_for<0, kSpanRing>(issue);
+  } else {
+    tag = ep % 65535u + 1u;
+    if (lane == 0) flag[0] = err != 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int pc = lane + 64 * i;
+      if (pc < PC)
+        *reinterpret_cast<u32x4*>(smem + G::kOffB + ((pc / (H / 8)) * G::ks(0) + 8 * (pc % (H / 8))) * 2) = attn_v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int pc = lane + 64 * i;
+      if (pc < H / 8) {
+        *reinterpret_cast<u32x4*>(smem + G::kOffLn + pc * 16) = lnp_v[i];
+        *reinterpret_cast<u32x4*>(smem + G::kOffLn + H * 2 + pc * 16) = lnn_v[i];
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  barrier_lds();
+  if (abort_now()) return;
+  PGS_SPAN_MARK(1);
+
+  // ================= stage 0: o_proj + residual =================
+  if (!control) run_stage(std::integral_constant<int, 0>{});
+  barrier_lds();
+  PGS_SPAN_MARK(2);
+  if (control) {
+    const int t = lane / 8, r = lane % 8;
+    if (lane < 8 * M && wg < H / 8) {
+      const float v = reduce(std::integral_constant<int, 0>{}, 0, 0, t, r) * so_r;
+      x1_r = bf16r(bf16r(v) + res_r);  // engine/model.py:184: residual + bf16(linear)
+      st_agent(x1x + wg * (kSlot / 4) + t * 8 + r, (tag << 16) | f32_to_bf16_bits(x1_r));
+    }
+    const uint32_t want = p.force_giveup ? tag % 65535u + 1u : tag;
+    if (!gather<M, H / 8>(x1x, ltag, want, p.spin_limit)) {
+      giveup();
+    } else if (wg == 0 && lane == 0) {
+      // every workgroup has read the epoch (it published with its tag)
+      st_agent(ws, tag);
+    }
+  }
+  barrier_lds();
+  if (abort_now()) return;
+  PGS_SPAN_MARK(3);
+  stage_b<M, H, G::ks(1), true>(smem, G::kOffTag, G::kOffB, G::kOffLn, G::kOffSsq, p.eps);
+  barrier_lds();
+  PGS_SPAN_MARK(4);
+
+  // ================= stage 1: gate|up, SwiGLU =================
+  if (!control) run_stage(std::integral_constant<int, 1>{});
+  barrier_lds();
+  PGS_SPAN_MARK(5);
+  if (control) {
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int idx = lane + 64 * i;
+      const int lu = idx / (8 * M), t = (idx / 8) % M, r = idx % 8;
+      const int g = wg + kSpanG * lu;
+      if (lu < G::U(1) && g < I / 8) {
+        const float gv = reduce(std::integral_constant<int, 1>{}, lu, 0, t, r) * sg_r[i];
+        const float uv = reduce(std::integral_constant<int, 1>{}, lu, 1, t, r) * su_r[i];
+        const float a = silu_f32(gv) * uv;
+        st_agent(actx + g * (kSlot / 4) + t * 8 + r, (tag << 16) | f32_to_bf16_bits(a));
+      }
+    }
+    if (!gather<M, I / 8>(actx, ltag, tag, p.spin_limit)) giveup();
+  }
+  barrier_lds();
+  if (abort_now()) return;
+  PGS_SPAN_MARK(6);
+  stage_b<M, I, G::ks(2), false>(smem, G::kOffTag, G::kOffB, G::kOffLn, G::kOffSsq, p.eps);
+  barrier_lds();
+  PGS_SPAN_MARK(7);
+
+  // ================= stage 2: down_proj + residual =================
+  if (!control) run_stage(std::integral_constant<int, 2>{});
+  barrier_lds();
+  PGS_SPAN_MARK(8);
+  if (control) {
+    const int t = lane / 8, r = lane % 8;
+    if (lane < 8 * M && wg < H / 8) {
+      const float v = reduce(std::integral_constant<int, 2>{}, 0, 0, t, r) * sd_r;
+      const float x2 = bf16r(bf16r(v) + x1_r);  // engine/model.py:190
+      const uint16_t bits = f32_to_bf16_bits(x2);
+      p.x_out[static_cast<int64_t>(t) * H + 8 * wg + r] = bits;
+      if (has_qkv) st_agent(x2x + wg * (kSlot / 4) + t * 8 + r, (tag << 16) | bits);
+    }
+    if (has_qkv && !gather<M, H / 8>(x2x, ltag, tag, p.spin_limit)) giveup();
+  }
+  barrier_lds();
+  if (!has_qkv || abort_now()) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  PGS_SPAN_MARK(9);
+  stage_b<M, H, G::ks(3), true>(smem, G::kOffTag, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, p.eps);
+  barrier_lds();
+  PGS_SPAN_MARK(10);
+
+  // ================= stage 3: q|k|v (+ bias), RoPE =================
+  if (!control) run_stage(std::integral_constant<int, 3>{});
+  barrier_lds();
+  PGS_SPAN_MARK(11);
+  if (control && lane < 8 * M) {
+    const int t = lane / 8, r = lane % 8;
+    int mem = 0, row0 = 0;
+    const URef u0 = unit_ref<DM, M, 3>(p, wg, 0, 0, &mem, &row0);
+    if (u0.ok) {
+      uint16_t* y = pick_early(p.yqkv, mem);
+      const int n = mem == 0 ? DM::NQ : DM::NKV;
+      const float y0 = bf16r(reduce(std::integral_constant<int, 3>{}, 0, 0, t, r) * sq_r[0] + bq_r[0]);
+      if (mem < 2) {
+        const float y1 = bf16r(reduce(std::integral_constant<int, 3>{}, 1, 0, t, r) * sq_r[1] + bq_r[1]);
+        float o0 = y0, o1 = y1;
+        if (p.cos) {
+          // engine/model.py:53-56 with rotate_half (:37-39), the reference's roundings
+          o0 = bf16r(bf16r(y0 * cs_r[0]) + bf16r(-y1 * cs_r[1]));
+          o1 = bf16r(bf16r(y1 * cs_r[2]) + bf16r(y0 * cs_r[3]));
+        }
+        y[static_cast<int64_t>(t) * n + qrow[0]] = f32_to_bf16_bits(o0);
+        y[static_cast<int64_t>(t) * n + qrow[1]] = f32_to_bf16_bits(o1);
+      } else {
+        y[static_cast<int64_t>(t) * n + qrow[0]] = f32_to_bf16_bits(y0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  PGS_SPAN_MARK(12);
+}
+
+// device CU counts, checked once per device (0 = not yet)
+std::atomic<int> g_cus[kMaxDevices];
+
+template <class DM, int M>
+int launch_span(const SpanParams& p, hipStream_t st, int dev) {
+  int cus = g_cus[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(PGS_ERR_NO_DEVICE, "pgs_w8a16_decode_span: cannot query device %d", dev);
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, span_kernel<DM, M>, kSpanThreads, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      per_cu = 0;
+    }
+    // one resident workgroup per CU, and exactly kSpanG CUs
+    cus = (per_cu == 1 && prop.multiProcessorCount == kSpanG) ? prop.multiProcessorCount : -1;
+    g_cus[dev].store(cus, std::memory_order_relaxed);
+  }
+  if (cus != kSpanG)
+    return fail(PGS_ERR_INVALID_ARGUMENT,
+                "pgs_w8a16_decode_span: the persistent launch needs %d CUs holding one workgroup each", kSpanG);
+  note_launch(__PRETTY_FUNCTION__, kSpanG, 1);
+  hipLaunchKernelGGL((span_kernel<DM, M>), dim3(kSpanG), dim3(kSpanThreads), 0, st, p);
+  return check_launch("w8a16 decode span kernel");
+}
+
+int g_spin_limit = 1 << 18;
+int g_force_giveup = 0;
+
+}  // namespace
+}  // namespace pgs
+
+using namespace pgs;
+
+extern "C" size_t pgs_w8a16_decode_span_workspace_bytes(int64_t m, int64_t hidden, int64_t inter) {
+  if (m < 1 || m > 4 || hidden <= 0 || inter <= 0 || hidden % 8 || inter % 8) return 0;
+  return static_cast<size_t>(kHeader) + static_cast<size_t>(2 * hidden / 8 + inter / 8) * kSlot;
+}
+
+extern "C" int pgs_w8a16_decode_span_supported(int64_t m, int64_t hidden, int64_t inter, int64_t nq, int64_t nkv,
+                                                int64_t head_dim) {
+  return (m >= 1 && m <= 2 && hidden == Qwen25_3B::H && inter == Qwen25_3B::I && nq == Qwen25_3B::NQ &&
+          nkv == Qwen25_3B::NKV && head_dim == Qwen25_3B::HD)
+             ? 1
+             : 0;
+}
+
+extern "C" int pgs_w8a16_decode_span_test_hooks(int spin_limit, int force_giveup) {
+  if (spin_limit < 0) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_w8a16_decode_span_test_hooks: negative spin limit");
+  g_spin_limit = spin_limit == 0 ? (1 << 18) : spin_limit;
+  g_force_giveup = force_giveup ? 1 : 0;
+  return PGS_OK;
+}
+
+extern "C" int pgs_w8a16_decode_span_status(void* workspace, int reset, void* stream) {
+  const char* fn = "pgs_w8a16_decode_span_status";
+  if (!workspace) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null workspace", fn);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = require_device(fn, st)) return rc;
+  uint32_t hdr[2] = {0, 0};
+  if (hipMemcpyAsync(hdr, workspace, sizeof(hdr), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    hipError_t e = hipGetLastError();
+    return fail(PGS_ERR_LAUNCH, "%s: reading the workspace header failed: %s", fn, hipGetErrorString(e));
+  }
+  if (hdr[1] == 0) return PGS_OK;
+  if (reset) {
+    // the caller passes the size it allocated; the header and exchange
+    // buffers start zero again (a kernel fill)
+    if (int rc = fill_zero(workspace, static_cast<int64_t>(kHeader) + 2 * (Qwen25_3B::H / 8) * kSlot +
+                                          (Qwen25_3B::I / 8) * kSlot, st))
+      return rc;
+  }
+  return fail(PGS_ERR_TIMEOUT, "%s: a decode span launch gave up waiting for another workgroup's outputs", fn);
+}
+
+extern "C" int pgs_w8a16_decode_span(const void* attn, const void* residual, void* x_out, const pgs_span_weights* w,
+                                     const pgs_span_next* next, float eps, int64_t m, int64_t hidden, int64_t inter,
+                                     void* workspace, size_t workspace_bytes_, void* stream) {
+  const char* fn = "pgs_w8a16_decode_span";
+  if (!w || !attn || !residual || !x_out || !workspace)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  const int64_t nq = next ? next->q.n : Qwen25_3B::NQ, nkv = next ? next->k.n : Qwen25_3B::NKV;
+  const int64_t hd = next ? next->head_dim : Qwen25_3B::HD;
+  if (!pgs_w8a16_decode_span_supported(m, hidden, inter, nq, nkv, hd))
+    return fail(PGS_ERR_INVALID_ARGUMENT,
+                "%s: no compiled configuration for m=%lld hidden=%lld inter=%lld q=%lld kv=%lld head_dim=%lld "
+                "(pgs_w8a16_decode_span_supported)",
+                fn, (long long)m, (long long)hidden, (long long)inter, (long long)nq, (long long)nkv, (long long)hd);
+  if (next && next->v.n != nkv) return fail(PGS_ERR_INVALID_ARGUMENT, "%s: k and v sizes differ", fn);
+  if (workspace_bytes_ < pgs_w8a16_decode_span_workspace_bytes(m, hidden, inter))
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes_,
+                pgs_w8a16_decode_span_workspace_bytes(m, hidden, inter));
+  const void* need16[] = {attn, residual, w->qp_o, w->qp_gate, w->qp_up, w->qp_down, w->ln_post};
+  for (const void* q : need16)
+    if (!q || !aligned(q, 16)) return fail(PGS_ERR_MISALIGNED, "%s: weights, norm weights and activations need 16-byte alignment", fn);
+  if (!w->s_o || !w->s_gate || !w->s_up || !w->s_down || !aligned(x_out, 2) || !aligned(workspace, 256))
+    return fail(PGS_ERR_INVALID_ARGUMENT, "%s: null scale, misaligned output or workspace", fn);
+  SpanParams p{};
+  p.attn = static_cast<const uint16_t*>(attn);
+  p.resid = static_cast<const uint16_t*>(residual);
+  p.x_out = static_cast<uint16_t*>(x_out);
+  p.qo = w->qp_o;
+  p.so = w->s_o;
+  p.ln_post = static_cast<const uint16_t*>(w->ln_post);
+  p.qg = w->qp_gate;
+  p.sg = w->s_gate;
+  p.qu = w->qp_up;
+  p.su = w->s_up;
+  p.qd = w->qp_down;
+  p.sd = w->s_down;
+  if (next) {
+    const pgs_linear_out* o[3] = {&next->q, &next->k, &next->v};
+    if (!next->ln_in || !aligned(next->ln_in, 16))
+      return fail(PGS_ERR_MISALIGNED, "%s: the next layer's norm weight must be 16-byte aligned", fn);
+    if ((next->cos == nullptr) != (next->sin == nullptr))
+      return fail(PGS_ERR_INVALID_ARGUMENT, "%s: cos and sin go together", fn);
+    p.ln_next = static_cast<const uint16_t*>(next->ln_in);
+    for (int j = 0; j < 3; ++j) {
+      if (!o[j]->qp || !o[j]->scale || !o[j]->y || !aligned(o[j]->qp, 16) || !aligned(o[j]->y, 2))
+        return fail(PGS_ERR_INVALID_ARGUMENT, "%s: q/k/v output %d lacks a weight, scale or output", fn, j);
+      p.qkv[j] = o[j]->qp;
+      p.sqkv[j] = o[j]->scale;
+      p.bqkv[j] = static_cast<const uint16_t*>(o[j]->bias);
+      p.yqkv[j] = static_cast<uint16_t*>(o[j]->y);
+    }
+    p.cos = static_cast<const uint16_t*>(next->cos);
+    p.sin = static_cast<const uint16_t*>(next->sin);
+  }
+  p.ws = static_cast<uint32_t*>(workspace);
+  p.eps = eps;
+  p.spin_limit = g_spin_limit;
+  p.force_giveup = g_force_giveup;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = require_device(fn, st)) return rc;
+  int dev = -1;
+  if (int rc = stream_device(st, &dev)) return rc;
+  if (m == 1) return launch_span<Qwen25_3B, 1>(p, st, dev);
+  return launch_span<Qwen25_3B, 2>(p, st, dev);
+}
