@@ -63,6 +63,9 @@
 #ifndef PGS_SPAN_MARK
 #define PGS_SPAN_MARK(i)
 #endif
+#ifndef PGS_SPAN_NOTE
+#define PGS_SPAN_NOTE(i, v)
+#endif
 
 namespace pgs {
 namespace {
@@ -102,19 +105,27 @@ struct Dims {
 using Qwen25_3B = Dims<2048, 11008, 2048, 256, 128>;
 
 // Stage geometry.  Stage 0: o_proj, 1: gate|up, 2: down_proj, 3: q|k|v.
-// A unit is 8 rows of one matrix over its whole K (half of a 16-row tile,
-// folded: two 64-k chunks per MFMA); an item is one 128-k slot of a unit
-// (one 1 KiB load per matrix); the items of a workgroup's units are dealt to
-// the streaming waves in contiguous runs of P.
+// A unit is R = 16 / F rows of one matrix over its whole K, folded: F 64-k
+// chunks per MFMA (A rows i of the tile's R-row group in chunk i / R, B
+// columns t + M j for the tokens' chunk j), as the skinny kernel's folded
+// halves; an item is one F*64-k slot of a unit (one 1 KiB load per matrix);
+// the items of a workgroup's units are dealt to the streaming waves in
+// contiguous runs of P.  F = 2 (8-row units) throughout: 4-row units
+// (F = 4) would balance gate|up better (10 or 11 units per workgroup instead
+// of 5 or 6) but read 64 of each 128 bytes of a cache line, the other half
+// belonging to another workgroup, often on another XCD: measured 31 against
+// 24.5 us per layer.
 template <class DM, int M>
 struct Geo {
   static constexpr int H = DM::H, I = DM::I;
   // q and k heads in unit pairs (rows i and i + HD/2 of a head, for RoPE), v
   // units alone
   static constexpr int kQP = DM::NQ / 16, kKP = DM::NKV / 16, kVS = DM::NKV / 8;
-  static constexpr int units(int s) { return s == 1 ? I / 8 : s == 3 ? (DM::NQ + 2 * DM::NKV) / 8 : H / 8; }
+  static constexpr int fold(int) { return 2; }
+  static constexpr int rows(int s) { return 16 / fold(s); }
+  static constexpr int units(int s) { return s == 1 ? I / rows(1) : s == 3 ? (DM::NQ + 2 * DM::NKV) / 8 : H / 8; }
   static constexpr int U(int s) { return s == 3 ? 2 : cdiv(units(s), kSpanG); }
-  static constexpr int ipu(int s) { return (s == 2 ? I : H) / 128; }
+  static constexpr int ipu(int s) { return (s == 2 ? I : H) / (64 * fold(s)); }
   static constexpr int kdim(int s) { return s == 2 ? I : H; }
   static constexpr int nl(int s) { return s == 1 ? 2 : 1; }
   static constexpr int P(int s) { return cdiv(U(s) * ipu(s), kSpanSW); }
@@ -128,20 +139,18 @@ struct Geo {
   // B operand rows in LDS: [M][K + 64] bf16 (the pad staggers the tokens)
   static constexpr int ks(int s) { return kdim(s) + 64; }
   static constexpr int kBBytes = M * (cmax(H, I) + 64) * 2;
-  // gathered exchange words, compact [unit][2M pieces of 16 B]
-  static constexpr int kTagBytes = cmax(H, I) * 4 * M;
   static constexpr int kPartFloats = kSpanSW * 2 * 2 * 8 * M;
   static constexpr int kOffB = 0;
-  static constexpr int kOffTag = kOffB + kBBytes;
-  static constexpr int kOffLn = kOffTag + kTagBytes;  // two norm weights [H] bf16
+  static constexpr int kOffLn = kOffB + kBBytes;  // two norm weights [H] bf16
   static constexpr int kOffPart = kOffLn + 2 * H * 2;
   static constexpr int kOffSsq = kOffPart + kPartFloats * 4;
   static constexpr int kOffFlag = kOffSsq + 16 * M * 4;
-  static constexpr int kLds = cmax(kOffFlag + 16, kMinLds);
+  static constexpr int kLds = cmax(kOffFlag + 32, kMinLds);
   static_assert(kLds <= 160 * 1024, "LDS of one workgroup");
   static_assert(P(0) <= ipu(0) && P(1) <= ipu(1) && P(2) <= ipu(2) && P(3) <= ipu(3),
                 "a wave's run touches at most two units");
   static_assert(8 * M * 4 <= kSlot, "a unit's outputs fit its exchange slot");
+  static_assert(fold(1) * M <= 16, "the folded token groups fit the MFMA's 16 columns");
 };
 
 // Kernel arguments (device pointers; see pgs_w8a16_decode_span).
@@ -172,10 +181,10 @@ struct SpanParams {
 };
 
 // Where a unit's weights are: its 16-row block row (whole K) and the byte
-// offset of its 8-row half inside a block.
+// offset of its rows inside a block.
 struct URef {
   const int8_t* blk;
-  int half;
+  int roff;
   bool ok;
 };
 
@@ -206,28 +215,48 @@ __device__ __forceinline__ URef unit_ref(const SpanParams& p, int wg, int lu, in
     if (member) *member = mem;
     if (row0) *row0 = unit * 8;
     u.blk = q + static_cast<int64_t>(unit >> 1) * (DM::H / 64) * 1024;
-    u.half = unit & 1;
+    u.roff = (unit & 1) * 128;
     u.ok = ok && q != nullptr;
   } else {
     const int g = wg + kSpanG * lu;
     const int8_t* q = S == 0 ? p.qo : S == 2 ? p.qd : (mat ? p.qu : p.qg);
     constexpr int kb = G::kdim(S) / 64;
-    if (row0) *row0 = g * 8;
-    u.blk = q + static_cast<int64_t>(g >> 1) * kb * 1024;
-    u.half = g & 1;
+    constexpr int R = G::rows(S), PER = 16 / R;  // units per 16-row tile
+    if (row0) *row0 = g * R;
+    u.blk = q + static_cast<int64_t>(g / PER) * kb * 1024;
+    u.roff = (g % PER) * R * 16;
     u.ok = g < G::units(S);
   }
   return u;
-}
-
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, kSC1);
 }
 
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// Whether any thread of the workgroup has `pred` set; all threads call it
+// and get the same answer.  (__syncthreads_or would also wait for every
+// outstanding vector load, the streaming waves' ring included.)  Three LDS
+// words in rotation, indexed by a workgroup-uniform sequence number `seq`
+// that the caller increments per call: the word for call seq + 1 is cleared
+// before this call's barrier, when every thread has read it (at call
+// seq - 2) and passed call seq - 1's barrier; the kernel zeroes all three
+// before its first call.
+typedef __attribute__((address_space(3))) int lds_int;
+
+__device__ __forceinline__ bool block_any(bool pred, int* words_generic, int& seq) {
+  // (explicitly LDS: a generic access would be a flat one, which the
+  // vector memory counter also tracks)
+  lds_int* words = (lds_int*)words_generic;
+  lds_int* w = words + seq % 3;
+  if (__any(pred) && (threadIdx.x & 63) == 0) __hip_atomic_fetch_or(w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (threadIdx.x == 0) __hip_atomic_store(words + (seq + 1) % 3, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  barrier_lds();
+  const bool any = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+  ++seq;
+  return any;
 }
 
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
@@ -239,106 +268,84 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 
-// Gathers every unit's tagged outputs of one exchange buffer into LDS
-// (compact [unit][2M pieces]) by LDS DMA, until every word carries `want`
-// (control wave only).  Each poll fetches only the pieces whose tags were
-// stale in the previous one (each lane keeps a bitmask of its pieces): a
-// CU's vector memory requests are served in order, so every byte a poll
-// fetches delays it and whatever follows it.  Returns false after
+// Gathers every unit's tagged outputs of one exchange buffer and builds the
+// next stage's B operand from them (all waves of the workgroup).  Thread
+// `tid` polls pieces tid + 1024 i (16 bytes: four words of one unit's
+// outputs of one token) into registers with agent-scope loads; a poll
+// refetches only the pieces whose tags were stale, and the workgroup stops
+// polling once no thread holds a stale piece.  A CU's vector memory
+// requests are served in order, so a poll waits behind whatever the CU has
+// queued: spreading it over all 16 waves keeps each wave's share short.
+// Then, NORM: rms_norm (engine/model.py:29-34) with the norm weight in LDS,
+// r = 1 / sqrt(mean(x^2) + eps), h = bf16(w * bf16(x * r)), the sum of
+// squares in a fixed order (per thread over its pieces, a wave butterfly,
+// the 16 waves in order); otherwise the values as they are.  The B operand
+// is [M][KS] bf16 in LDS.  Returns false (the same for every thread) after
 // spin_limit polls.
-template <int M, int NUNITS>
-__device__ __forceinline__ bool gather(const uint32_t* xbuf, unsigned char* lds_tag, uint32_t want, int spin_limit) {
-  constexpr int NP = NUNITS * 2 * M, NI = cdiv(NP, 64), NW = cdiv(NI, 32);
-  const int lane = threadIdx.x & 63;
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(xbuf, static_cast<int64_t>(NUNITS) * kSlot);
-  uint32_t stale[NW];
+template <int M, int K, int KS, bool NORM, class OnPoll>
+__device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* smem, int off_b, int off_ln,
+                                         int off_ssq, int* any_words, int& seq, uint32_t want, int spin_limit,
+                                         float eps, int& polls, OnPoll&& on_poll) {
+  constexpr int NP = (K / 8) * 2 * M, NPT = cdiv(NP, kSpanThreads);
+  static_assert(NPT <= 32, "one stale bit per piece");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(xbuf, static_cast<int64_t>(K / 8) * kSlot);
+  auto piece_off = [&](int i) {
+    const int pc = tid + kSpanThreads * i;
+    return pc < NP ? (pc / (2 * M)) * kSlot + (pc % (2 * M)) * 16 : 0x7ffffff0;
+  };
+  auto fresh = [&](const u32x4& x) {
+    return (x[0] >> 16) == want && (x[1] >> 16) == want && (x[2] >> 16) == want && (x[3] >> 16) == want;
+  };
+  // Each wave polls until its own pieces are fresh, and only then issues
+  // (on_poll) the next stage's first loads: a wave's loads return in
+  // order, so a poll issued behind its own weight loads would wait for
+  // them.  Then the workgroup-wide check (which also makes a give-up
+  // uniform).
+  u32x4 v[NPT];
+  uint32_t stale = 0;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) stale[w] = 0xffffffffu;
+  for (int i = 0; i < NPT; ++i)
+    if (tid + kSpanThreads * i < NP) stale |= 1u << i;
   for (int spin = 0;; ++spin) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int pc = lane + 64 * i;
-      if (stale[i / 32] & (1u << (i % 32))) {
-        const int off = pc < NP ? (pc / (2 * M)) * kSlot + (pc % (2 * M)) * 16 : 0x7ffffff0;
-        dma16(r, lds_tag + i * 1024, off);
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    bool left = false;
+    for (int i = 0; i < NPT; ++i)
+      if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int pc = lane + 64 * i;
-      if (stale[i / 32] & (1u << (i % 32))) {
-        bool ok = pc >= NP;
-        if (!ok) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(lds_tag + pc * 16);
-          ok = (v[0] >> 16) == want && (v[1] >> 16) == want && (v[2] >> 16) == want && (v[3] >> 16) == want;
-        }
-        if (ok) stale[i / 32] &= ~(1u << (i % 32));
-        left |= !ok;
-      }
-    }
-    if (!__any(left)) return true;
-    if (spin >= spin_limit) return false;
+    for (int i = 0; i < NPT; ++i)
+      if ((stale & (1u << i)) && fresh(v[i])) stale &= ~(1u << i);
+    polls = spin + 1;
+    if (!__any(stale != 0) || spin >= spin_limit) break;
     __builtin_amdgcn_s_sleep(1);
   }
-}
-
-// Word index of (token t, row n) in the compact gathered layout.
-template <int M>
-__device__ __forceinline__ int tag_word(int t, int n) {
-  return (n >> 3) * (8 * M) + t * 8 + (n & 7);
-}
-
-// All waves: B operand of the next stage from the gathered words.  NORM:
-// rms_norm (engine/model.py:29-34) with the norm weight in LDS:
-// r = 1 / sqrt(mean(x^2) + eps), h = bf16(w * bf16(x * r)); the sum of
-// squares in a fixed order (per thread, then a wave butterfly, then the 16
-// waves in order).  Two barriers when NORM (the wave sums meet in LDS).
-template <int M, int K, int KS, bool NORM>
-__device__ __forceinline__ void stage_b(unsigned char* smem, int off_tag, int off_b, int off_ln, int off_ssq,
-                                        float eps) {
-  constexpr int E = M * K / 2;  // dwords (bf16 pairs)
-  constexpr int NE = cdiv(E, kSpanThreads);
-  const uint32_t* tw = reinterpret_cast<const uint32_t*>(smem + off_tag);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t w0[NE], w1[NE];
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int e = tid + kSpanThreads * i;
-    const int t = e / (K / 2), n = 2 * (e % (K / 2));
-    if (e < E) {
-      const int wi = tag_word<M>(t, n);
-      w0[i] = tw[wi];
-      w1[i] = tw[wi + 1];
-    } else {
-      w0[i] = w1[i] = 0;
-    }
-  }
-  float r[M];
+  on_poll();
+  if (block_any(stale != 0, any_words, seq)) return false;
+  // piece pc: unit pc / 2M (rows 8 unit ..), token (pc % 2M) / 2, rows
+  // 8 unit + 4 (pc % 2) + e for its words e = 0..3
+  float r_t[M];
   if constexpr (NORM) {
     float ss[M];
 #pragma unroll
     for (int t = 0; t < M; ++t) ss[t] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NE; ++i) {
-      const int e = tid + kSpanThreads * i;
-      const int t = e / (K / 2);
-      const float a = bf16_bits_to_f32(w0[i] & 0xffffu), b = bf16_bits_to_f32(w1[i] & 0xffffu);
+    for (int i = 0; i < NPT; ++i) {
+      const int pc = tid + kSpanThreads * i;
+      const int t = (pc % (2 * M)) / 2;
 #pragma unroll
-      for (int tt = 0; tt < M; ++tt)
-        if (e < E && t == tt) {
-          ss[tt] += a * a;
-          ss[tt] += b * b;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const float x = bf16_bits_to_f32(v[i][e] & 0xffffu);
+#pragma unroll
+        for (int tt = 0; tt < M; ++tt)
+          if (pc < NP && t == tt) ss[tt] += x * x;
+      }
     }
     float* ssq = reinterpret_cast<float*>(smem + off_ssq);
 #pragma unroll
     for (int t = 0; t < M; ++t) {
-      float v = ss[t];
+      float x = ss[t];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-      if (lane == 0) ssq[wave * M + t] = v;
+      for (int o = 1; o < 64; o <<= 1) x += __shfl_xor(x, o);
+      if (lane == 0) ssq[wave * M + t] = x;
     }
     barrier_lds();
 #pragma unroll
@@ -346,28 +353,33 @@ __device__ __forceinline__ void stage_b(unsigned char* smem, int off_tag, int of
       float tot = 0.f;
 #pragma unroll
       for (int w = 0; w < 16; ++w) tot += ssq[w * M + t];
-      r[t] = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+      r_t[t] = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
     }
   }
-  const uint16_t* ln = reinterpret_cast<const uint16_t*>(smem + off_ln);
-  uint32_t* bdst = reinterpret_cast<uint32_t*>(smem + off_b);
 #pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int e = tid + kSpanThreads * i;
-    if (e >= E) continue;
-    const int t = e / (K / 2), n = 2 * (e % (K / 2));
-    uint32_t out;
+  for (int i = 0; i < NPT; ++i) {
+    const int pc = tid + kSpanThreads * i;
+    if (pc >= NP) continue;
+    const int t = (pc % (2 * M)) / 2, n0 = (pc / (2 * M)) * 8 + (pc % 2) * 4;
+    u32x2 out;
     if constexpr (NORM) {
-      float rt = r[0];
+      float rt = r_t[0];
 #pragma unroll
-      for (int tt = 1; tt < M; ++tt) rt = t == tt ? r[tt] : rt;
-      const float a = bf16_bits_to_f32(w0[i] & 0xffffu), b = bf16_bits_to_f32(w1[i] & 0xffffu);
-      out = pack_bf16x2(bf16_bits_to_f32(ln[n]) * bf16r(a * rt), bf16_bits_to_f32(ln[n + 1]) * bf16r(b * rt));
+      for (int tt = 1; tt < M; ++tt) rt = t == tt ? r_t[tt] : rt;
+      const u32x2 w2 = *reinterpret_cast<const u32x2*>(smem + off_ln + n0 * 2);
+      float h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wb = (e & 1) ? (w2[e >> 1] >> 16) : (w2[e >> 1] & 0xffffu);
+        h[e] = bf16_bits_to_f32(wb) * bf16r(bf16_bits_to_f32(v[i][e] & 0xffffu) * rt);
+      }
+      out = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
     } else {
-      out = (w0[i] & 0xffffu) | (w1[i] << 16);
+      out = u32x2{(v[i][0] & 0xffffu) | (v[i][1] << 16), (v[i][2] & 0xffffu) | (v[i][3] << 16)};
     }
-    bdst[(t * KS + n) >> 1] = out;
+    *reinterpret_cast<u32x2*>(smem + off_b + (t * KS + n0) * 2) = out;
   }
+  return true;
 }
 
 template <class DM, int M, int RING = kSpanRingDefault>
@@ -380,9 +392,9 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool control = wave == kSpanSW;
   const bool has_qkv = p.ln_next != nullptr;
-  int* flag = reinterpret_cast<int*>(smem + G::kOffFlag);  // [0] abort
+  int* flag = reinterpret_cast<int*>(smem + G::kOffFlag);  // [0] abort, [1] the launch's tag, [4..6] block_any
+  int any_seq = 0;
   float* part = reinterpret_cast<float*>(smem + G::kOffPart);
-  unsigned char* ltag = smem + G::kOffTag;
   uint32_t* const ws = p.ws;
   uint32_t* const x1x = ws + kHeader / 4;
   uint32_t* const actx = x1x + (H / 8) * (kSlot / 4);
@@ -390,11 +402,13 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
 
   // ---- streaming-wave state -------------------------------------------
   const int lrow = lane & 15, kgrp = lane >> 4;
-  // A operand: this lane's 16 bytes of a fold slot (rows of the unit's half
-  // in chunk 2j + lrow / 8); B operand: column lrow = token lrow % M of chunk
-  // 2j + lrow / M (columns past 2M read token 0, unused)
-  const int avoff = (lrow >> 3) * 1024 + ((lrow & 7) + 16 * kgrp) * 16;
-  const int btok = lrow < 2 * M ? lrow % M : 0, bsub = lrow < 2 * M ? lrow / M : 0;
+  // A operand (fold F, R = 16 / F rows): this lane's 16 bytes of a fold
+  // slot, row lrow % R of the unit in chunk F j + lrow / R; B operand:
+  // column lrow = token lrow % M of chunk F j + lrow / M (columns past F M
+  // read token 0, unused)
+  auto avoff = [&](int f) { return (lrow / (16 / f)) * 1024 + ((lrow % (16 / f)) + 16 * kgrp) * 16; };
+  auto btok = [&](int f) { return lrow < f * M ? lrow % M : 0; };
+  auto bsub = [&](int f) { return lrow < f * M ? lrow / M : 0; };
   constexpr int kSpanRing = RING;
   u32x4 ring[kSpanRing];
   f32x4 acc[2][2];
@@ -407,10 +421,22 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
       const int item = G::P(S) * wave + it;
       const int lu = item / G::ipu(S), slot = item - lu * G::ipu(S);
       const URef u = unit_ref<DM, M, S>(p, wg, lu, mat, nullptr, nullptr);
-      const bool ok = u.ok && item < G::U(S) * G::ipu(S);
+      // (the control wave issues the same loads with an empty range: no
+      // memory access, but both roles then have the same loads in flight
+      // where their code paths join, so the compiler's waits stay exact)
+      const bool ok = !control && u.ok && item < G::U(S) * G::ipu(S);
       const __amdgpu_buffer_rsrc_t r = make_rsrc(ok ? u.blk : p.qo, ok ? (G::kdim(S) / 64) * 1024 : 0);
-      ring[li % kSpanRing] = __builtin_amdgcn_raw_buffer_load_b128(r, avoff, uniform(slot * 2048 + u.half * 128), kLoadNT);
+      constexpr int F = G::fold(S);
+      ring[li % kSpanRing] =
+          __builtin_amdgcn_raw_buffer_load_b128(r, avoff(F), uniform(slot * F * 1024 + u.roff), kLoadNT);
     }
+  };
+  // the first kSpanRing loads of stage S (the rest follow as its items are
+  // consumed): issued right behind the gather that stage S waits for, so
+  // that they stream in while the gather completes instead of delaying it
+  auto prime = [&](auto SI) {
+    constexpr int S = decltype(SI)::value;
+    static_for<G::lb(S), cmin(G::lb(S) + kSpanRing, G::lb(S + 1))>(issue);
   };
   auto zero_acc = [&] {
 #pragma unroll
@@ -424,15 +450,16 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     constexpr int S = decltype(SI)::value;
     const int first = G::P(S) * wave;
     const int lu0 = first / G::ipu(S);
-    const unsigned char* bbase = smem + G::kOffB + (btok * G::ks(S) + bsub * 64 + 16 * kgrp) * 2;
+    constexpr int F = G::fold(S), R = G::rows(S);
+    const unsigned char* bbase = smem + G::kOffB + (btok(F) * G::ks(S) + bsub(F) * 64 + 16 * kgrp) * 2;
     static_for<0, G::P(S)>([&](auto IT) {
       constexpr int it = decltype(IT)::value;
       const int item = first + it;
       const int lu = item / G::ipu(S), slot = item - lu * G::ipu(S);
       const bool ok = unit_ref<DM, M, S>(p, wg, lu, 0, nullptr, nullptr).ok && item < G::U(S) * G::ipu(S);
       if (ok) {
-        const u32x4 b0 = *reinterpret_cast<const u32x4*>(bbase + slot * 256);
-        const u32x4 b1 = *reinterpret_cast<const u32x4*>(bbase + slot * 256 + 16);
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(bbase + slot * F * 128);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(bbase + slot * F * 128 + 16);
         const bf16x8 x0 = __builtin_bit_cast(bf16x8, b0), x1 = __builtin_bit_cast(bf16x8, b1);
         const bool second = lu != lu0;
         static_for<0, G::nl(S)>([&](auto MT) {
@@ -449,21 +476,30 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
         });
       }
       static_for<0, G::nl(S)>([&](auto MT) {
-        issue(std::integral_constant<int, G::lb(S) + it * G::nl(S) + decltype(MT)::value + kSpanRing>{});
+        constexpr int nxt = G::lb(S) + it * G::nl(S) + decltype(MT)::value + kSpanRing;
+        if constexpr (nxt < G::lb(S + 1)) issue(std::integral_constant<int, nxt>{});
       });
     });
     // partial tiles: output (token t, row r) of a folded unit is
-    // C[r][t] + C[r + 8][t + M]; C[i][j] sits in lane 16 (i / 4) + j,
-    // register i % 4
+    // sum_s C[r + R s][t + M s] (s < F, in order); C[i][j] sits in lane
+    // 16 (i / 4) + j, register i % 4.  F = 2: lanes t and 16 + t hold rows
+    // 0-3 and 4-7, partners 32 + M lanes on; F = 4: lane t holds rows 0-3,
+    // partners 16 + M, 2 (16 + M), 3 (16 + M) lanes on.
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int mat = 0; mat < G::nl(S); ++mat) {
         f32x4 v = acc[a][mat];
+        constexpr int step = F == 2 ? 32 + M : 16 + M;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += __shfl_down(v[i], 32 + M);
+        for (int i = 0; i < 4; ++i) {
+          float x = v[i];
+#pragma unroll
+          for (int sft = 1; sft < F; ++sft) x += __shfl_down(v[i], sft * step);
+          v[i] = x;
+        }
         const int t = lane & 15;
-        if (lane < 32 && t < M) {
+        if (lane < 16 * (R / 4) && t < M) {
           float* dst = part + ((wave * 2 + a) * 2 + mat) * (8 * M) + t * 8 + (lane >> 4) * 4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) dst[i] = v[i];
@@ -476,7 +512,9 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   // outputs per lane: o / down: (t, r) = (idx / 8, idx % 8) of this
   // workgroup's unit; gate|up: idx = (lu, t, r); q|k|v: (t, r) of the unit
   // (pair)
-  constexpr int NO = cdiv(8 * M, 64), NG = cdiv(G::U(1) * 8 * M, 64);
+  // gate|up outputs of this workgroup: idx = (lu, t, r), r < R1 rows
+  constexpr int R1 = G::rows(1);
+  constexpr int NO = cdiv(8 * M, 64), NG = cdiv(G::U(1) * R1 * M, 64);
   static_assert(NO == 1, "one o/down output per control lane");
   uint32_t tag = 0;
   float so_r = 0.f, sd_r = 0.f, res_r = 0.f, x1_r = 0.f;
@@ -496,12 +534,6 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     }
     return v;
   };
-  auto giveup = [&] {
-    if (lane == 0) {
-      st_agent(ws + 1, 1u);
-      flag[0] = 1;
-    }
-  };
   auto abort_now = [&] {
     if (flag[0]) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -512,9 +544,10 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
 
   PGS_SPAN_MARK(0);
   // ================= prologue =================
-  // The control wave's loads go first: they are served before any weight
-  // load of this CU (a barrier orders the streaming waves' first loads
-  // after them), so the launch's operands are not queued behind the ring.
+  // The control wave's operand loads and the streaming waves' o_proj weight
+  // loads go out together (o_proj is 16 KiB per CU; the deeper weight
+  // stream starts only behind the gathers, whose polls must not queue
+  // behind it).
   constexpr int PC = M * H / 8, NA = cdiv(PC, 64), NL = cdiv(H / 8, 64);
   u32x4 attn_v[NA], lnp_v[NL], lnn_v[NL];
   uint32_t ep = 0, err = 0;
@@ -543,10 +576,10 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
       const int idx = lane + 64 * i;
-      const int lu = idx / (8 * M), r = idx % 8;
-      const int g = cmin(wg + kSpanG * lu, I / 8 - 1);
-      sg_r[i] = p.sg[8 * g + r];
-      su_r[i] = p.su[8 * g + r];
+      const int lu = idx / (R1 * M), r = idx % R1;
+      const int g = cmin(wg + kSpanG * lu, I / R1 - 1);
+      sg_r[i] = p.sg[R1 * g + r];
+      su_r[i] = p.su[R1 * g + r];
     }
     if (has_qkv) {
       const int t = cmin(lane / 8, M - 1), r = lane % 8;
@@ -575,14 +608,17 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
         cs_r[3] = bf16_bits_to_f32(p.sin[base + i + HD / 2]);
       }
     }
-  }
-  barrier_lds();
-  if (!control) {
-    zero_acc();
-    static_for<0, kSpanRing>(issue);
   } else {
+    zero_acc();
+    prime(std::integral_constant<int, 0>{});
+  }
+  if (control) {
     tag = ep % 65535u + 1u;
-    if (lane == 0) flag[0] = err != 0;
+    if (lane == 0) {
+      flag[0] = err != 0;
+      flag[1] = static_cast<int>(tag);
+      flag[4] = flag[5] = flag[6] = 0;
+    }
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int pc = lane + 64 * i;
@@ -604,6 +640,13 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   PGS_SPAN_MARK(1);
 
   // ================= stage 0: o_proj + residual =================
+  const uint32_t ltag = static_cast<uint32_t>(flag[1]);  // every wave's copy of the tag
+  int polls = 0;
+  // the whole workgroup gave up waiting: the error word, then out
+  auto give_up = [&] {
+    if (tid == 0) st_agent(ws + 1, 1u);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
   if (!control) run_stage(std::integral_constant<int, 0>{});
   barrier_lds();
   PGS_SPAN_MARK(2);
@@ -612,20 +655,21 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     if (lane < 8 * M && wg < H / 8) {
       const float v = reduce(std::integral_constant<int, 0>{}, 0, 0, t, r) * so_r;
       x1_r = bf16r(bf16r(v) + res_r);  // engine/model.py:184: residual + bf16(linear)
-      st_agent(x1x + wg * (kSlot / 4) + t * 8 + r, (tag << 16) | f32_to_bf16_bits(x1_r));
+      st_agent(x1x + wg * (kSlot / 4) + t * 8 + r, (ltag << 16) | f32_to_bf16_bits(x1_r));
     }
-    const uint32_t want = p.force_giveup ? tag % 65535u + 1u : tag;
-    if (!gather<M, H / 8>(x1x, ltag, want, p.spin_limit)) {
-      giveup();
-    } else if (wg == 0 && lane == 0) {
-      // every workgroup has read the epoch (it published with its tag)
-      st_agent(ws, tag);
-    }
+    PGS_SPAN_MARK(3);
   }
   barrier_lds();
-  if (abort_now()) return;
-  PGS_SPAN_MARK(3);
-  stage_b<M, H, G::ks(1), true>(smem, G::kOffTag, G::kOffB, G::kOffLn, G::kOffSsq, p.eps);
+  if (!gather_b<M, H, G::ks(1), true>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
+                                      p.force_giveup ? ltag % 65535u + 1u : ltag, p.spin_limit, p.eps, polls, [&] {
+                                        prime(std::integral_constant<int, 1>{});
+                                      })) {
+    give_up();
+    return;
+  }
+  // every workgroup has read the epoch (it published with its tag)
+  if (wg == 0 && tid == 0) st_agent(ws, ltag);
+  PGS_SPAN_NOTE(13, polls);
   barrier_lds();
   PGS_SPAN_MARK(4);
 
@@ -637,21 +681,28 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
       const int idx = lane + 64 * i;
-      const int lu = idx / (8 * M), t = (idx / 8) % M, r = idx % 8;
+      const int lu = idx / (R1 * M), t = (idx / R1) % M, r = idx % R1;
       const int g = wg + kSpanG * lu;
-      if (lu < G::U(1) && g < I / 8) {
+      if (lu < G::U(1) && g < I / R1) {
         const float gv = reduce(std::integral_constant<int, 1>{}, lu, 0, t, r) * sg_r[i];
         const float uv = reduce(std::integral_constant<int, 1>{}, lu, 1, t, r) * su_r[i];
         const float a = silu_f32(gv) * uv;
-        st_agent(actx + g * (kSlot / 4) + t * 8 + r, (tag << 16) | f32_to_bf16_bits(a));
+        // row R1 g + r lives in the 8-row exchange slot of its rows
+        const int row = R1 * g + r;
+        st_agent(actx + (row >> 3) * (kSlot / 4) + t * 8 + (row & 7), (ltag << 16) | f32_to_bf16_bits(a));
       }
     }
-    if (!gather<M, I / 8>(actx, ltag, tag, p.spin_limit)) giveup();
+    PGS_SPAN_MARK(6);
   }
   barrier_lds();
-  if (abort_now()) return;
-  PGS_SPAN_MARK(6);
-  stage_b<M, I, G::ks(2), false>(smem, G::kOffTag, G::kOffB, G::kOffLn, G::kOffSsq, p.eps);
+  if (!gather_b<M, I, G::ks(2), false>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
+                                       p.spin_limit, p.eps, polls, [&] {
+        prime(std::integral_constant<int, 2>{});
+      })) {
+    give_up();
+    return;
+  }
+  PGS_SPAN_NOTE(14, polls);
   barrier_lds();
   PGS_SPAN_MARK(7);
 
@@ -666,17 +717,23 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
       const float x2 = bf16r(bf16r(v) + x1_r);  // engine/model.py:190
       const uint16_t bits = f32_to_bf16_bits(x2);
       p.x_out[static_cast<int64_t>(t) * H + 8 * wg + r] = bits;
-      if (has_qkv) st_agent(x2x + wg * (kSlot / 4) + t * 8 + r, (tag << 16) | bits);
+      if (has_qkv) st_agent(x2x + wg * (kSlot / 4) + t * 8 + r, (ltag << 16) | bits);
     }
-    if (has_qkv && !gather<M, H / 8>(x2x, ltag, tag, p.spin_limit)) giveup();
+    PGS_SPAN_MARK(9);
   }
-  barrier_lds();
-  if (!has_qkv || abort_now()) {
+  if (!has_qkv) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
-  PGS_SPAN_MARK(9);
-  stage_b<M, H, G::ks(3), true>(smem, G::kOffTag, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, p.eps);
+  barrier_lds();
+  if (!gather_b<M, H, G::ks(3), true>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
+                                      ltag, p.spin_limit, p.eps, polls, [&] {
+                                        prime(std::integral_constant<int, 3>{});
+                                      })) {
+    give_up();
+    return;
+  }
+  PGS_SPAN_NOTE(15, polls);
   barrier_lds();
   PGS_SPAN_MARK(10);
 
