@@ -1,24 +1,31 @@
 """Benchmark of the INT8 weight-only (W8A16) linear path on one MI355X.
 
 Workload (one "step"): the linear projections of one decode token through
-all 36 layers of a Qwen2.5-3B-shaped model -- per layer q|k|v (2048+256+256
-rows, K=2048, with bias) as one grouped launch, o (2048x2048), gate|up
-(2x 11008x2048) as one fused SwiGLU launch, down (2048x11008) -- on distinct
-synthetic int8 weights per layer (2.77 GB, far beyond the 256 MB MALL),
-activations ~N(0,1) bf16 resident in HBM.  The 144 launches of a step are
-captured once in a HIP graph and replayed.
+all 36 layers of a Qwen2.5-3B-shaped model, as a dependent chain with the
+neighbours a real decode step runs between them (attention output fixed):
+layer 0's RMSNorm + q|k|v (with bias) + RoPE, then per layer o + residual,
+RMSNorm, gate|up (2x 11008x2048, SwiGLU), down (2048x11008) + residual and the
+next layer's RMSNorm + q|k|v + RoPE -- one persistent launch per layer where a
+single-launch configuration exists (one or two tokens), the per-projection
+kernels otherwise -- on distinct synthetic int8 weights per layer (2.77 GB,
+far beyond the 256 MB MALL), activations ~N(0,1) bf16 resident in HBM.  The
+launches of a step are captured once in a HIP graph and replayed.  Bytes are
+the linears' algorithmic bytes (the norms and RoPE are not counted).
 
 Reported (one JSON line on stdout):
   value          whole-sweep algorithmic GB/s at M=1 (int8 W + fp32 scale +
                  bf16 x + bf16 y + bf16 bias, as the launches read/write them)
-  roofline       the dominant kernel (fused gate|up at M=1): algorithmic bytes
-                 per launch / mean launch time from HIP events, vs 8 TB/s
+  roofline       the dominant kernel (the one launch per layer at M=1):
+                 algorithmic bytes per launch / mean launch time from HIP
+                 events, vs 8 TB/s
   prefill        the same sweep at M=512 in TFLOP/s vs the 2.5 PFLOP/s bf16
                  dense MFMA peak, with its own dominant-kernel roofline
   per_call_sweep the reference's call structure (7 separate linears/layer)
-  decode_detail  eager (no graph) time, the down_proj roofline, and one layer
-                 with its neighbours: RMSNorm inside the projections, as
-                 separate kernels, and as the reference's torch op chains
+  decode_detail  eager (no graph) time; the same chain with per-projection
+                 kernels (norm inside the projections, as separate kernels,
+                 and as the reference's torch op chains); the independent
+                 four-launch sweep on fixed inputs; the gate|up and down_proj
+                 kernels' rooflines
   other_configs  decode at M=4 and 16, prefill at M=128 and 2048, the fused
                  SwiGLU MLP, the int8 lm_head at M=1/8/256 (fp32 logits) and
                  the single 4864x896 linear beside its CPU reference path
@@ -94,12 +101,17 @@ def fused_sweep(layers, x, xo, m):
             outs.append(L["down"].linear(act))
         return outs
 
-    per_layer_b = (linear_bytes(m, HIDDEN + 2 * KV, HIDDEN, bias=True)           # q|k|v, x read once
-                   + linear_bytes(m, HIDDEN, HIDDEN)                             # o
-                   + 2 * INTER * HIDDEN + 8 * INTER + 2 * m * HIDDEN + 2 * m * INTER  # gate|up -> act
-                   + linear_bytes(m, HIDDEN, INTER))                             # down
     per_layer_f = 2 * m * HIDDEN * (HIDDEN + 2 * KV + HIDDEN + 2 * INTER) + 2 * m * INTER * HIDDEN
-    return step, per_layer_b * len(layers), per_layer_f * len(layers), 4 * len(layers)
+    return step, layer_bytes(m) * len(layers), per_layer_f * len(layers), 4 * len(layers)
+
+
+def layer_bytes(m):
+    """Algorithmic bytes of one layer's linears: q|k|v with bias (x read
+    once), o, gate|up -> act, down (int8 W + fp32 scale + bf16 x and y)."""
+    return (linear_bytes(m, HIDDEN + 2 * KV, HIDDEN, bias=True)
+            + linear_bytes(m, HIDDEN, HIDDEN)
+            + 2 * INTER * HIDDEN + 8 * INTER + 2 * m * HIDDEN + 2 * m * INTER
+            + linear_bytes(m, HIDDEN, INTER))
 
 
 def per_call_sweep(layers, x, xo, xi, m):
@@ -269,6 +281,42 @@ def layer_chain(layers, x0, attn, norms, rope, mode):
     return step
 
 
+def decode_chain(layers, x0, attn, norms, rope, m):
+    """The headline decode sweep: the linear path of one decode step through
+    every layer, each stage data-dependent on the one before (attention
+    output fixed, engine/model.py:165-190): layer 0's norm -> q|k|v (+ bias)
+    -> RoPE, then per layer o + residual -> norm -> gate|up -> down +
+    residual -> the next layer's norm -> q|k|v -> RoPE.  Where a single-launch
+    configuration exists (pageserve_amd.span) each layer's part between two
+    attention calls is one persistent launch; otherwise the per-projection
+    kernels.  Returns (step, algorithmic bytes, launches, single_launch)."""
+    from pageserve_amd import quantization as Q
+    from pageserve_amd import span as S
+
+    cos, sin = rope
+    single = S.span_supported(m, HIDDEN, INTER, HIDDEN, KV, 128)
+
+    def step():
+        L0 = layers[0]
+        q, k, v = Q.rmsnorm_linear_group(x0, norms[0][0], 1e-6, [L0["q"], L0["k"], L0["v"]],
+                                         [L0["q_b"], L0["k_b"], L0["v_b"]])
+        Q.rope_qk(q.view(m, -1, 128), k.view(m, -1, 128), cos, sin, inplace=True)
+        x = x0
+        outs = [q, k, v]
+        for i, L in enumerate(layers):
+            N = layers[i + 1] if i + 1 < len(layers) else None
+            kw = {} if N is None else dict(next_ln=norms[i + 1][0], next_qkv=(N["q"], N["k"], N["v"]),
+                                           next_bias=(N["q_b"], N["k_b"], N["v_b"]), cos=cos, sin=sin)
+            x, qkv = S.decode_span(attn, x, L["o"], norms[i][1], L["gate"], L["up"], L["down"], 1e-6, **kw)
+            if qkv is not None:
+                outs = list(qkv)
+        return [x] + outs
+
+    nbytes = len(layers) * layer_bytes(m)
+    launches = 2 + (len(layers) if single else 5 * len(layers) - 2)
+    return step, nbytes, launches, single
+
+
 def capture(fn):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -350,6 +398,7 @@ PMC_KERNELS = {
     "copy": r"neg_kernel",
     "skinny_gate_up_m1": r"skinny_kernel<(\d+, )?\d+, \d+, 2, false",
     "gemm_gate_up_m512": r"gemm_(dma|k64)_kernel<(\d+, )?\d+, 2, false|gemm_kernel<(\d+, )?\d+, 2, false",
+    "span_m1": r"span_kernel",
 }
 
 
@@ -371,7 +420,17 @@ def pmc_workload(dev, layers_n):
         for L in layers:
             Q.swiglu(x, L["gate"], L["up"])
         torch.cuda.synchronize()
-    log(f"[bench] pmc workload done: copy x3, gate|up m=1 and m=512 x {layers_n} layers")
+    # the single launch per layer of the decode chain at one token
+    from pageserve_amd import span as S
+
+    x = torch.randn((1, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    ln = torch.ones(HIDDEN, device=dev, dtype=torch.bfloat16)
+    for i, L in enumerate(layers):
+        N = layers[(i + 1) % len(layers)]
+        S.decode_span(x, x, L["o"], ln, L["gate"], L["up"], L["down"], 1e-6, next_ln=ln,
+                      next_qkv=(N["q"], N["k"], N["v"]), next_bias=(N["q_b"], N["k_b"], N["v_b"]))
+    torch.cuda.synchronize()
+    log(f"[bench] pmc workload done: copy x3, gate|up m=1 and m=512, decode span m=1 x {layers_n} layers")
 
 
 def _pmc_means(dirs):
@@ -678,6 +737,62 @@ def _sha(a) -> str:
     return hashlib.sha256(a.tobytes()).hexdigest()[:16]
 
 
+def span_gate(dev, layers, l, ref_q, norms, rope, x, attn, O, np32):
+    """Layer l's single-launch decode span (o + residual, norm, gate|up,
+    down + residual, the next layer's norm + q|k|v + bias, RoPE) against the
+    oracle, each stage on its own GPU input (the launch's exchanged
+    intermediates); the fused RoPE bit for bit against the oracle's RoPE of
+    the same launch's un-rotated q and k."""
+    import numpy as np
+
+    from pageserve_amd import span as S
+
+    L = layers[l]
+    m = x.shape[0]
+    N = layers[l + 1] if l + 1 < len(layers) else None
+    kw = {}
+    nq = {}
+    if N is not None:
+        for j, name in enumerate(("q", "k", "v")):
+            n, k = SHAPES[name]
+            nq[name] = O.quantize_per_channel(layer_weight(dev, l + 1, j, n, k).cpu().numpy())
+        kw = dict(next_ln=norms[l + 1][0], next_qkv=(N["q"], N["k"], N["v"]), next_bias=(N["q_b"], N["k_b"], N["v_b"]))
+    x_out, qkv = S.decode_span(attn, x, L["o"], norms[l][1], L["gate"], L["up"], L["down"], 1e-6, **kw)
+    torch.cuda.synchronize()
+    x1, act, tags = S.exchange_values(m, HIDDEN, INTER)
+    x1, act = x1.numpy(), act.numpy()
+    xn, an, xo_ = np32(x), np32(attn), np32(x_out)
+    ln2, ln1 = np32(norms[l][1]), np32(norms[l + 1][0]) if N is not None else None
+    res = []
+
+    def check(name, y, ref, k, **bound):
+        r = O.compare(y, ref, k, bf16_out=True, **bound)
+        res.append({"layer": l, "m": m, "launch": f"span {name}", "ok": r["ok"], "rel": round(r["rel"], 6),
+                    "worst_vs_bound": round(r["worst_vs_bound"], 4), "rows": m})
+
+    check("o + residual", x1, O.linear_residual(an, *ref_q["o"], xn), HIDDEN,
+          ulp_of=O.linear_residual_intermediate(an, *ref_q["o"]))
+    h2, dh2 = O.rmsnorm(x1, ln2, 1e-6), O.rmsnorm_dx(x1, ln2, 1e-6)
+    check("gate|up", act, O.swiglu(h2, *ref_q["gate"], *ref_q["up"]), HIDDEN,
+          acc=O.swiglu_acc(h2, *ref_q["gate"], *ref_q["up"], dx=dh2))
+    check("down + residual", xo_, O.linear_residual(act, *ref_q["down"], x1), INTER,
+          ulp_of=O.linear_residual_intermediate(act, *ref_q["down"]))
+    ok_tags = len(tags) == 1 and 0 not in tags
+    if N is not None:
+        h1, dh1 = O.rmsnorm(xo_, ln1, 1e-6), O.rmsnorm_dx(xo_, ln1, 1e-6)
+        for y, name in zip(qkv, ("q", "k", "v")):
+            b = np32(N[name + "_b"])
+            check(name, np32(y), O.linear(h1, *nq[name], b), HIDDEN, acc=O.acc_bound(h1, *nq[name], b, dx=dh1))
+        _, rot = S.decode_span(attn, x, L["o"], norms[l][1], L["gate"], L["up"], L["down"], 1e-6, cos=rope[0],
+                               sin=rope[1], **kw)
+        cs, sn = np32(rope[0]), np32(rope[1])
+        rope_ok = all(np.array_equal(np32(r_).reshape(m, -1), O.rope(np32(u_).reshape(m, -1, 128), cs, sn).reshape(m, -1))
+                      for r_, u_ in zip(rot[:2], qkv[:2])) and bool(torch.equal(rot[2], qkv[2]))
+        res.append({"layer": l, "m": m, "launch": "span RoPE (bit-exact)", "ok": bool(rope_ok), "rows": m})
+    res.append({"layer": l, "m": m, "launch": "span exchange tags", "ok": ok_tags, "rows": m})
+    return res
+
+
 def correctness_gate(dev, layers, inputs, check_layers):
     """After the timed runs: the same launches as the timed sweeps, on the
     same weights and inputs, against the oracle (oracle/quantization_oracle.py
@@ -697,6 +812,8 @@ def correctness_gate(dev, layers, inputs, check_layers):
         return t.detach().float().cpu().numpy()
 
     out = {"ok": True, "quantizer": [], "linears": []}
+    inputs = dict(inputs)
+    span = inputs.pop("span", None)
     for l in check_layers:
         L = layers[l]
         ref_q = {}
@@ -731,6 +848,14 @@ def correctness_gate(dev, layers, inputs, check_layers):
                 out["linears"].append({"layer": l, "m": m, "launch": name, "ok": r["ok"], "rel": round(r["rel"], 6),
                                        "worst_vs_bound": round(r["worst_vs_bound"], 4), "rows": len(rows)})
                 out["ok"] &= r["ok"]
+        if span is not None:
+            from pageserve_amd import span as S
+
+            norms, rope, sx, sattn = span
+            if S.span_supported(sx.shape[0], HIDDEN, INTER, HIDDEN, KV, 128):
+                for r in span_gate(dev, layers, l, ref_q, norms, rope, sx, sattn, O, np32):
+                    out["linears"].append(r)
+                    out["ok"] &= r["ok"]
     return out
 
 
@@ -840,19 +965,52 @@ def main():
         xi = torch.randn((m, INTER), generator=gen, device=dev).to(torch.bfloat16)
         if args.only in ("all", "decode"):
             gate_inputs[m] = (x, xo)
-            step, nbytes, nflops, launches = fused_sweep(layers, x, xo, m)
+            # norm weights and the rotary rows of the reference's cache
+            # (engine/model.py:42-47) at one position per token
+            ng = torch.Generator(device=dev).manual_seed(77)
+            norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
+                           for _ in range(2)) for _ in layers]
+            inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, device=dev).float() / 128))
+            emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
+            rope = (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
+            gate_inputs["span"] = (norms, rope, x, xo)
+            # the headline: the dependent decode chain
+            step, nbytes, launches, single = decode_chain(layers, x, xo, norms, rope, m)
             eager_out = step()
             g, graph_out = capture(step)
             g.replay()
             torch.cuda.synchronize()
-            for a, b in zip(eager_out, graph_out):
-                assert torch.equal(a, b), "graph replay differs from eager"
-            log("[bench] decode sweep captured; timing")
+            for a_, b_ in zip(eager_out, graph_out):
+                assert torch.equal(a_, b_), "graph replay differs from eager"
+            log("[bench] decode chain captured; timing")
             ms = time_graph(g, args.steps, args.warmup)
             ms_eager = time_eager(step, max(5, args.steps // 10), 3)
             value = nbytes / (ms * 1e-3) / 1e9
-            log(f"[bench] decode m={m}: {ms * 1e3:.1f} us/sweep, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% "
-                f"of HBM peak); eager {ms_eager * 1e3:.1f} us")
+            log(f"[bench] decode m={m} (dependent chain, {'one launch per layer' if single else 'per-projection kernels'}): "
+                f"{ms * 1e3:.1f} us/sweep, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak); "
+                f"eager {ms_eager * 1e3:.1f} us")
+            del g
+            # the same chain with the per-projection kernels, and with the
+            # reference's torch op chains for the neighbours
+            chain = {}
+            for mode in ("reference", "kernels", "norm_in_linear"):
+                cg, _ = capture(layer_chain(layers, x, xo, norms, rope, mode))
+                chain[mode] = time_graph(cg, max(20, args.steps // 4), 5) * 1e3 / len(layers)
+                del cg
+            chain_eager = time_eager(layer_chain(layers, x, xo, norms, rope, "norm_in_linear"),
+                                     max(5, args.steps // 10), 3) * 1e3 / len(layers)
+            log(f"[bench] decode chain per-projection kernels (us/layer): norm in the linear {chain['norm_in_linear']:.2f}"
+                f" (eager {chain_eager:.2f}), separate kernels {chain['kernels']:.2f}, reference structure "
+                f"{chain['reference']:.2f}")
+            # the independent four-launch sweep (every launch on fixed inputs)
+            istep, ibytes, _, ilaunches = fused_sweep(layers, x, xo, m)
+            ig, _ = capture(istep)
+            ims = time_graph(ig, args.steps, args.warmup)
+            ims_eager = time_eager(istep, max(5, args.steps // 10), 3)
+            ival = ibytes / (ims * 1e-3) / 1e9
+            log(f"[bench] independent sweep (4 launches/layer, fixed inputs): {ims * 1e3:.1f} us, {ival:.1f} GB/s; "
+                f"eager {ims_eager * 1e3:.1f} us")
+            del ig
             pstep, pbytes, _, plaunch = per_call_sweep(layers, x, xo, xi, m)
             pg, _ = capture(pstep)
             pms = time_graph(pg, args.steps, args.warmup)
@@ -862,48 +1020,65 @@ def main():
             dms_eager = time_eager(dstep, max(5, args.steps // 10), 3)
             log(f"[bench] per-call sweep (7 launches/layer): {pms * 1e3:.1f} us graph, {pms_eager * 1e3:.1f} us eager; "
                 f"through F.linear(x, W.get(), b) eagerly: {dms_eager * 1e3:.1f} us")
-            del g, pg
+            del pg
             ref_ms = dense_ms = None
             if not args.no_torch_ref:
                 ref_ms, dense_ms = torch_reference_sweeps(layers, x, xo, max(10, args.steps // 10))
                 log(f"[bench] reference computation with torch on this GPU: dequantize + F.linear "
                     f"{ref_ms * 1e3:.1f} us, dense bf16 F.linear {dense_ms * 1e3:.1f} us per sweep")
+            # dominant kernel of the headline: the single launch per layer
+            if single:
+                from pageserve_amd import span as S
+
+                nxt = {id(L): layers[(i + 1) % len(layers)] for i, L in enumerate(layers)}
+
+                def span_launch(L):
+                    N = nxt[id(L)]
+                    return S.decode_span(xo, x, L["o"], norms[0][1], L["gate"], L["up"], L["down"], 1e-6,
+                                         next_ln=norms[0][0], next_qkv=(N["q"], N["k"], N["v"]),
+                                         next_bias=(N["q_b"], N["k_b"], N["v_b"]), cos=rope[0], sin=rope[1])
+
+                roof = kernel_roofline(layers, span_launch, layer_bytes(m),
+                                       2 * m * HIDDEN * (2 * HIDDEN + 3 * INTER + 2 * KV), "hbm")
+                roof["kernel"] = ("span_kernel (o + residual, RMSNorm, gate|up SwiGLU, down + residual, RMSNorm, "
+                                  "next layer's q|k|v + bias + RoPE: one launch per layer)")
+                roof["traffic"] = read_traffic("span_m1") if m == 1 else None
             swiglu_b = 2 * INTER * HIDDEN + 8 * INTER + 2 * m * HIDDEN + 2 * m * INTER
-            roof = kernel_roofline(layers, lambda L: Q.swiglu(x, L["gate"], L["up"]), swiglu_b,
-                                   4 * m * INTER * HIDDEN, "hbm")
-            roof["kernel"] = "skinny_kernel<NMAT=2> (fused gate|up, 2x[11008,2048] int8)"
-            roof["traffic"] = read_traffic("skinny_gate_up_m1") if m == 1 else None
+            gu_roof = kernel_roofline(layers, lambda L: Q.swiglu(x, L["gate"], L["up"]), swiglu_b,
+                                      4 * m * INTER * HIDDEN, "hbm")
+            gu_roof["kernel"] = "skinny_kernel<NMAT=2> (fused gate|up, 2x[11008,2048] int8)"
+            gu_roof["traffic"] = read_traffic("skinny_gate_up_m1") if m == 1 else None
+            if not single:
+                roof = gu_roof
             log(f"[bench] dominant kernel: {roof['launch_us']} us/launch, {roof['achieved']} GB/s")
             down_roof = kernel_roofline(layers, lambda L: L["down"].linear(xi), linear_bytes(m, HIDDEN, INTER),
                                         2 * m * HIDDEN * INTER, "hbm")
-            # the layer chain with its neighbours, fused vs the reference's structure
-            ng = torch.Generator(device=dev).manual_seed(77)
-            norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
-                           for _ in range(2)) for _ in layers]
-            # rotary tables of the reference's cache (engine/model.py:42-47), one position
-            inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, device=dev).float() / 128))
-            emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
-            rope = (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
-            chain = {}
-            for mode in ("reference", "kernels", "norm_in_linear"):
-                cg, _ = capture(layer_chain(layers, x, xo, norms, rope, mode))
-                chain[mode] = time_graph(cg, max(20, args.steps // 4), 5) * 1e3 / len(layers)
-                del cg
-            log(f"[bench] decode layer chain with neighbours (us/layer): norm in the linear {chain['norm_in_linear']:.2f}"
-                f", separate kernels {chain['kernels']:.2f}, reference structure {chain['reference']:.2f}")
             result.update({
                 "value": round(value, 2), "ms_per_step": round(ms, 5), "roofline": roof,
-                "decode_detail": {"frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+                "decode_detail": {"what": ("dependent decode chain: layer 0's norm + q|k|v + RoPE, then per layer "
+                                           "o + residual, norm, gate|up, down + residual, the next layer's norm + "
+                                           "q|k|v + bias + RoPE (attention output fixed); HIP-graph replay"),
+                                  "single_launch_per_layer": single,
+                                  "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                                   "bytes_per_step": nbytes, "launches_per_step": launches,
                                   "eager_ms_per_step": round(ms_eager, 5),
                                   "eager_gbs": round(nbytes / (ms_eager * 1e-3) / 1e9, 2),
-                                  "down_proj_roofline": down_roof,
-                                  "layer_chain_with_neighbours": {
-                                      "what": "per layer: rmsnorm, q|k|v, RoPE of q and k, o + residual, rmsnorm, "
-                                              "gate|up, down + residual (attention output fixed); HIP-graph replay",
-                                      "fused_us_per_layer": round(chain["norm_in_linear"], 3),
+                                  "per_projection_chain": {
+                                      "what": "the same chain with per-projection kernels (norm inside q|k|v and "
+                                              "gate|up, RoPE kernel, residual epilogues), 5 launches per layer",
+                                      "us_per_layer": round(chain["norm_in_linear"], 3),
+                                      "eager_us_per_layer": round(chain_eager, 3),
                                       "separate_norm_kernel_us_per_layer": round(chain["kernels"], 3),
-                                      "reference_structure_us_per_layer": round(chain["reference"], 3)}},
+                                      "reference_structure_us_per_layer": round(chain["reference"], 3)},
+                                  "independent_sweep": {
+                                      "what": "q|k|v, o, gate|up, down per layer on fixed inputs (no norms, no "
+                                              "RoPE), 4 launches per layer",
+                                      "ms_per_step": round(ims, 5), "gbs": round(ival, 2),
+                                      "frac_of_hbm_peak": round(ival / HBM_PEAK_GBS, 4),
+                                      "bytes_per_step": ibytes, "launches_per_step": ilaunches,
+                                      "eager_ms_per_step": round(ims_eager, 5)},
+                                  "gate_up_roofline": gu_roof,
+                                  "down_proj_roofline": down_roof},
                 "per_call_sweep": {"ms_per_step": round(pms, 5), "gbs": round(pval, 2),
                                    "frac_of_hbm_peak": round(pval / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": pbytes, "launches_per_step": plaunch,
@@ -996,9 +1171,11 @@ def main():
         "value": result.get("value"), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": result.get("ms_per_step"), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"Qwen2.5-3B decode linears, {args.layers} layers x (q|k|v grouped with bias, o, "
-                               f"gate|up fused SwiGLU, down), M={args.m}, int8 per-row weights from N(0,0.02), "
-                               f"HIP-graph replay",
+        "config": {"workload": f"Qwen2.5-3B decode linears as a dependent chain: {args.layers} layers x (o + "
+                               f"residual, RMSNorm, gate|up SwiGLU, down + residual, the next layer's RMSNorm + "
+                               f"q|k|v with bias + RoPE; attention output fixed), M={args.m}, int8 per-row weights "
+                               f"from N(0,0.02), HIP-graph replay; bytes = the linears' int8 W + fp32 scale + bf16 "
+                               f"x/y",
                    "m": args.m, "layers": args.layers, "hidden": HIDDEN, "intermediate": INTER, "kv_dim": KV,
                    "weight_dtype": "int8", "activation_dtype": "bf16", "accumulate": "fp32",
                    "parallelism": "none (1 GPU)"},

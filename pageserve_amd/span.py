@@ -198,3 +198,27 @@ def _chain(attn, residual, o, ln_post, gate, up, down, eps, next_ln, next_qkv, n
         k3 = k.reshape(m, -1, head_dim)
         Q.rope_qk(q3, k3, cos, sin, inplace=True)
     return x, (q, k, v)
+
+
+def exchange_values(m: int, hidden: int, inter: int, device: torch.device | None = None):
+    """(x1, act): the residual stream after o_proj and the SwiGLU activations
+    of the last single-launch :func:`decode_span` call on the current stream
+    (the values its workgroups exchanged), as float32 ``[m, hidden]`` and
+    ``[m, inter]`` CPU tensors, and the set of launch tags seen in them (one
+    tag when every word comes from that launch).  For checks of each stage
+    on its own GPU input; synchronises the stream."""
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    ws = _eager.get((dev.index, Q._raw_stream(dev)))
+    if ws is None:
+        raise RuntimeError("decode_span: no single-launch call on this stream yet")
+    w = ws.view(torch.int32).cpu().to(torch.int64) & 0xFFFFFFFF
+    hdr = 256 // 4
+
+    def unpack(base, units):
+        blk = w[base: base + units * 32].reshape(units, 32)[:, : 8 * m].reshape(units, m, 8)
+        vals = (blk & 0xFFFF).to(torch.int32).to(torch.int16).view(torch.bfloat16).float()
+        return vals.permute(1, 0, 2).reshape(m, units * 8), set((blk >> 16).unique().tolist())
+
+    x1, t1 = unpack(hdr, hidden // 8)
+    act, t2 = unpack(hdr + (hidden // 8) * 32, inter // 8)
+    return x1, act, t1 | t2
