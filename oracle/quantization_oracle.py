@@ -300,14 +300,15 @@ def swiglu_acc(x, q_gate, s_gate, q_up, s_up, dx=None) -> np.ndarray:
     errors dg, du; act = silu(g) * u moves by at most |silu'| dg |u| +
     |silu(g)| du + dg du (|silu'| <= 1.1 everywhere; its value at g is used),
     and the fp32 evaluation of silu (exp, add, divide) and the product add
-    at most 16 u |act|.  ``dx`` as for :func:`acc_bound`."""
+    at most (16 + |g| log2 e) u |act|: the exp2 argument -g log2 e is itself
+    rounded, an error that grows with |g|.  ``dx`` as for :func:`acc_bound`."""
     g = linear(x, q_gate, s_gate).astype(np.float64)
     u = linear(x, q_up, s_up).astype(np.float64)
     dg = acc_bound(x, q_gate, s_gate, dx=dx)
     du = acc_bound(x, q_up, s_up, dx=dx)
     sig = 1.0 / (1.0 + np.exp(-g))
     dsilu = np.abs(sig * (1.0 + g * (1.0 - sig))) + dg  # the slope anywhere within dg of g (|silu''| <= 0.5)
-    return dsilu * dg * np.abs(u) + np.abs(g * sig) * du + dg * du + 16 * U32 * np.abs(g * sig * u)
+    return dsilu * dg * np.abs(u) + np.abs(g * sig) * du + dg * du + (16 + np.abs(g) * 1.4426950408889634) * U32 * np.abs(g * sig * u)
 
 
 def mlp_acc(x, q_gate, s_gate, q_up, s_up, q_down, s_down) -> np.ndarray:

@@ -66,10 +66,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 
 // x * sigmoid(x) in fp32 (F.silu): x / (1 + e^-x) with the hardware
 // base-2 exponential (v_exp_f32, e^-x = 2^(-x log2 e)) and the hardware
-// reciprocal (v_rcp_f32), each within about one fp32 ulp: a few ulps in all,
-// far below the bf16 rounding of the result, in about 5 instructions
-// instead of the library exponential and IEEE division (~30).  x -> +inf:
-// x; x -> -inf: -0 (NaN at -inf itself, as x * sigmoid(x) gives).
+// reciprocal (v_rcp_f32), each within about one fp32 ulp, in about 5
+// instructions instead of the library exponential and IEEE division (~30).
+// The rounding of the exponent y = -x log2 e (half an ulp of |y|) scales
+// e^-x by up to 2^(|y| u / 2), so the relative error is about
+// (4 + |x| log2 e) ulps: a few ulps for the |x| of a layer's gate values,
+// more where e^-x is huge (x far below zero, silu(x) then tiny).
+// x -> +inf: x; x -> -inf: -0 (NaN at -inf itself, as x * sigmoid(x) gives).
 __device__ __forceinline__ float silu_f32(float x) {
   const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
   return x * __builtin_amdgcn_rcpf(1.0f + e);

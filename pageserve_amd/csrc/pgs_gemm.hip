@@ -85,13 +85,23 @@ __device__ __forceinline__ Rows4<NMAT> rows4(const GroupArgs& a, int g, int N, i
   const float* sc0 = (NMAT == 2) ? a.scale[0] : pick(a.scale, g);
   const float* sc1 = a.scale[NMAT - 1];
   const uint16_t* bias = (NMAT == 2) ? nullptr : pick(a.bias, g);
+  // the bias is loaded unconditionally (an absent one reads the scales as a
+  // dummy address) and selected afterwards: a load under a branch makes the
+  // compiler wait for every earlier load, the kernels' activation DMAs
+  // included, before continuing
+  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(sc0);
   Rows4<NMAT> e;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int n = min(nb + r, N - 1);
     e.s0[r] = sc0[n];
     e.s1[r] = (NMAT == 2) ? sc1[n] : 0.f;
-    e.bv[r] = (NMAT == 1 && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
+    if constexpr (NMAT == 1) {
+      const float bvr = bf16_bits_to_f32(bsrc[n]);
+      e.bv[r] = bias ? bvr : 0.f;
+    } else {
+      e.bv[r] = 0.f;
+    }
   }
   return e;
 }
@@ -953,6 +963,9 @@ __global__ __launch_bounds__(1024) void gemm_once_kernel(const uint16_t* __restr
       dma16(xres, xs + sl * 512, row * K * 2 + c * 128 + lc * 16, 0);
     }
   }
+  // the vmcnt wait below counts on the DMAs being issued before everything
+  // else: keep the scheduler from moving later loads above them
+  __builtin_amdgcn_sched_barrier(0);
   // epilogue operands
   const int lr = lane & 15, lg = lane >> 4;
   const int nb = n0 + nt * 16 + 4 * lg;
@@ -1163,7 +1176,10 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
   // 57.3-58.8, at 1280 69.8 vs 79.3 and at 1536 78.7 vs 87-90 with four, at
   // 2048 94.5 vs 99-104 with two; at 512 and 1024 tokens within noise of the
   // plans below, at 256 no faster)
-  const bool long128 = can_split && nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m > 256;
+  // (without a workspace only where the split would stop at one anyway, 512
+  // tiles and more, so that a call plans alike with or without one)
+  const bool long128 = nmat == 1 && k % kBK == 0 && p.bn == kBN && kb > 64 && m > 256 &&
+                       (can_split || tiles_for(128) >= 512);
   if (long128) p.bm = 128;
   // a single matrix with a short K and few 64-token tiles: 32-token tiles
   // give the CUs work without splitting K

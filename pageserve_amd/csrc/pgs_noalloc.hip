@@ -74,8 +74,11 @@ extern "C" int pgs_w8a16_linear_noalloc(const void* x, const int8_t* qp, const f
       return fail(PGS_ERR_INVALID_ARGUMENT, "%s: m=%lld n=%lld k=%lld needs %zu bytes of scratch, above the %zu-byte maximum",
                   fn, (long long)m, (long long)n, (long long)k, need, kScratchBytes);
   }
+  // the scratch goes to every non-empty call, so its plan is the one
+  // pgs_w8a16_linear makes with a workspace (some plans need none but are
+  // only taken where a split would be possible)
   void* ws = nullptr;
-  if (need) {
+  if (m > 0 && n > 0 && k > 0) {
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (int rc = require_device(fn, st)) return rc;
     int dev = -1;

@@ -49,7 +49,9 @@ def _reference_call(lib, x, qp, sc, b, y, m, n, k, stream):
 # matrix (32 x 64 tiles, K split 4) then o_proj at 160 tokens (32 x 64, unsplit)
 PAIRS = [((200, 2048, 11008), (9, 2048, 2048)), ((5, 2048, 11008), (1, 2048, 11008)),
          ((150, 300, 4160), (40, 200, 4160)), ((1920, 2048, 11008), (1280, 2048, 11008)),
-         ((200, 100, 2048), (160, 2048, 2048))]
+         ((200, 100, 2048), (160, 2048, 2048)),
+         # down_proj at 4096 tokens: 128 x 128 tiles, no split, no scratch needed
+         ((4096, 2048, 11008), (2304, 2048, 11008))]
 
 
 @pytest.mark.parametrize("first,second", PAIRS)
@@ -86,3 +88,65 @@ def test_noalloc_rejects_plans_beyond_its_scratch(gpu):
     rc = _noalloc(lib)(VP(256), VP(256), VP(256), None, VP(256), 1, m, n, k,
                                       VP(torch.cuda.current_stream().cuda_stream))
     assert rc == 1 and b"maximum" in lib.pgs_last_error()
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+from helpers import activations, bf16_gpu, weights
+from pageserve_amd import _native
+from pageserve_amd import quantization as Q
+lib = _native.load()
+VP = ctypes.c_void_p
+dev = torch.device("cuda", 0)
+m, n, k = 200, 2048, 11008
+qw = Q.QuantizedWeight(torch.from_numpy(weights(931, n, k)).to(dev))
+qp, sc = qw._kernel_operands()
+x = bf16_gpu(activations(932, m, k), dev)
+y_ref = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+need = lib.pgs_w8a16_workspace_bytes(m, (ctypes.c_int64 * 1)(n), 1, k, 0)
+assert need > 0
+ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+st = torch.cuda.current_stream().cuda_stream
+assert lib.pgs_w8a16_linear(VP(x.data_ptr()), VP(qp.data_ptr()), VP(sc.data_ptr()), None, VP(y_ref.data_ptr()), 1,
+                            m, n, k, VP(ws.data_ptr()), need, VP(st)) == 0
+y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    # the first call on this device in this process: takes the scratch
+    # address and clears its pair slots inside the capture
+    rc = lib.pgs_w8a16_linear_noalloc(VP(x.data_ptr()), VP(qp.data_ptr()), VP(sc.data_ptr()), None,
+                                      VP(y.data_ptr()), 1, m, n, k, VP(s.cuda_stream))
+assert rc == 0, lib.pgs_last_error()
+torch.cuda.current_stream().wait_stream(s)
+y_eager = torch.empty_like(y)
+for rep in range(4):
+    y.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), f"replay {rep} differs from pgs_w8a16_linear"
+    # an eager call in between on the same stream, sharing the scratch
+    assert lib.pgs_w8a16_linear_noalloc(VP(x.data_ptr()), VP(qp.data_ptr()), VP(sc.data_ptr()), None,
+                                        VP(y_eager.data_ptr()), 1, m, n, k, VP(st)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y_eager, y_ref), f"eager call {rep} differs"
+print("capture ok")
+"""
+
+
+def test_noalloc_first_call_inside_a_graph_capture(gpu):
+    """In a fresh process, the first call of the entry point is made inside
+    a HIP graph capture (split-K plan): the scratch address is taken and the
+    pair slots cleared during the capture; every replay, with eager calls on
+    the same stream between replays, equals pgs_w8a16_linear bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parent.parent)
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and "capture ok" in res.stdout, res.stdout[-2000:] + res.stderr[-2000:]
