@@ -613,12 +613,14 @@ def mfma_summary(pmc_dir, plan_path, command):
     return "\n".join(lines) + "\n"
 
 
-def other_configs(layers, dev, steps):
+def other_configs(layers, dev, steps, gate_inputs=None):
     """The remaining workload sizes, one compact figure each: decode sweeps at
     M=4 and 16, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
     and 512, the int8 lm_head [151936, 2048] at M=1, 8 and 256 (two copies
     alternated so the 256 MB MALL cannot hold the weight), and the single
-    [4864, 896] linear at M=1 with the reference's CPU path beside it."""
+    [4864, 896] linear at M=1 with the reference's CPU path beside it.  The
+    sweeps' and the MLP's inputs are added to ``gate_inputs`` for the
+    correctness gate."""
     from pageserve_amd import quantization as Q
 
     gen = torch.Generator(device=dev).manual_seed(4242)
@@ -627,8 +629,11 @@ def other_configs(layers, dev, steps):
         return torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
 
     out = {}
+    gate_inputs = {} if gate_inputs is None else gate_inputs
     for m in (4, 16):
-        step, nbytes, _, _ = fused_sweep(layers, act(m, HIDDEN), act(m, HIDDEN), m)
+        x, xo = act(m, HIDDEN), act(m, HIDDEN)
+        gate_inputs[m] = (x, xo)
+        step, nbytes, _, _ = fused_sweep(layers, x, xo, m)
         g, _ = capture(step)
         ms = time_graph(g, steps, 3)
         gbs = nbytes / (ms * 1e-3) / 1e9
@@ -636,7 +641,9 @@ def other_configs(layers, dev, steps):
                                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         del g
     for m in (128, 2048):
-        step, _, nflops, _ = fused_sweep(layers, act(m, HIDDEN), act(m, HIDDEN), m)
+        x, xo = act(m, HIDDEN), act(m, HIDDEN)
+        gate_inputs[m] = (x, xo)
+        step, _, nflops, _ = fused_sweep(layers, x, xo, m)
         g, _ = capture(step)
         ms = time_graph(g, max(5, steps // 4), 2)
         tf = nflops / (ms * 1e-3) / 1e12
@@ -645,6 +652,7 @@ def other_configs(layers, dev, steps):
         del g
     for m in (1, 512):
         x = act(m, HIDDEN)
+        gate_inputs[("mlp", m)] = x
         g, _ = capture(lambda: [Q.mlp(x, L["gate"], L["up"], L["down"]) for L in layers])
         ms = time_graph(g, max(5, steps // 4), 2)
         per = ms * 1e3 / len(layers)
@@ -801,7 +809,8 @@ def correctness_gate(dev, layers, inputs, check_layers):
     sha256 prefixes recorded), and at each token count every launch kind of
     the sweep -- q|k|v with bias, o, the fused gate|up, down on the kernel's
     own gate|up output -- within the specification's tolerance (all rows at
-    up to 16 tokens, 16 sampled rows above)."""
+    up to 16 tokens, 16 sampled rows above); for ``("mlp", m)`` keys the
+    fused MLP (gate|up then down) against the oracle's fp32 MLP."""
     import numpy as np
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -825,7 +834,19 @@ def correctness_gate(dev, layers, inputs, check_layers):
                                      "scale_sha256": _sha(sg)})
             out["ok"] &= ok
             ref_q[name] = (qr, sr)
-        for m, (x, xo) in inputs.items():
+        for m, xs in inputs.items():
+            if isinstance(m, tuple):  # ("mlp", tokens): Q.mlp as other_configs times it
+                x = xs
+                rows = np.arange(m[1]) if m[1] <= 16 else np.linspace(0, m[1] - 1, 16).astype(int)
+                xn = np32(x)[rows]
+                w3 = (*ref_q["gate"], *ref_q["up"], *ref_q["down"])
+                y = Q.mlp(x, L["gate"], L["up"], L["down"])
+                r = O.compare(np32(y)[rows], O.mlp(xn, *w3), INTER, bf16_out=True, acc=O.mlp_acc(xn, *w3))
+                out["linears"].append({"layer": l, "m": m[1], "launch": "mlp", "ok": r["ok"], "rel": round(r["rel"], 6),
+                                       "worst_vs_bound": round(r["worst_vs_bound"], 4), "rows": len(rows)})
+                out["ok"] &= r["ok"]
+                continue
+            x, xo = xs
             rows = np.arange(m) if m <= 16 else np.linspace(0, m - 1, 16).astype(int)
             xn, xon = np32(x)[rows], np32(xo)[rows]
             outs = Q.linear_group(x, [L["q"], L["k"], L["v"]], [L["q_b"], L["k_b"], L["v_b"]])
@@ -1123,7 +1144,7 @@ def main():
 
         # ---------------- the other workload sizes ----------------
         if args.only in ("all", "configs") and not args.no_configs:
-            oc = other_configs(layers, dev, args.steps)
+            oc = other_configs(layers, dev, args.steps, gate_inputs)
             for key, v in oc.items():
                 log(f"[bench] {key}: {v}")
             result["other_configs"] = oc

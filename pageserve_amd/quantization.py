@@ -23,15 +23,22 @@ Explicit entry points that the reference's call sites can use directly:
 :func:`swiglu` (gate/up/silu*up in one launch, engine/model.py:188-190).
 
 Device placement follows the reference: results live where the input lives.
-All arithmetic runs on the GPU; a CPU-resident weight is staged to the current
-GPU for the kernel and the result copied back.  Without a GPU or without the
-built library every entry point raises (there is no CPU implementation).
+GPU tensors always run the gfx950 HIP kernels; without the built library those
+calls raise.  CPU tensors keep the reference's own math, evaluated by torch on
+the CPU (the reference quantizes on the CPU, engine/model.py:101-112, and its
+one ``quantize=True`` caller runs a CPU fp32 model,
+scripts/verify_quantization.py:32): a CPU weight is quantized, stored,
+unpacked and dequantized there without any copy to a GPU, and ``get()``
+returns the dense dequantized weight as the reference's does.  The fused
+entry points (``linear``, ``linear_group``, ``swiglu`` ...) take GPU tensors
+only.
 """
 
 from __future__ import annotations
 
 import ctypes
 import functools
+import threading
 from collections import OrderedDict
 
 import torch
@@ -63,15 +70,6 @@ _DTYPE_CODE = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float
 # ---------------------------------------------------------------------------
 # plumbing
 # ---------------------------------------------------------------------------
-
-def _require_gpu() -> torch.device:
-    if not torch.cuda.is_available():
-        raise RuntimeError(
-            "pageserve_amd: no ROCm GPU is visible; the INT8 linear path runs only on the "
-            "gfx950 HIP kernels (there is no CPU implementation)"
-        )
-    return torch.device("cuda", torch.cuda.current_device())
-
 
 # torch's current stream as a raw hipStream_t, without building a Stream
 # object per call (the public route costs a few microseconds of host time)
@@ -136,6 +134,10 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 #    call shares it.  It is a temporary of the graph's memory pool and leaves
 #    this table once its capture is over.
 _MAX_EAGER_WS = 16  # (device, stream) pairs kept; the least recently used is dropped
+# The tables are shared by every thread: each lookup-and-update holds this
+# lock (calls from several threads on one stream then share that stream's
+# buffer, which the stream's order makes safe).
+_ws_lock = threading.Lock()
 _eager_ws: "OrderedDict[tuple[int, int], torch.Tensor]" = OrderedDict()
 _capture_ws: dict[tuple[int, int], tuple[int, torch.Tensor]] = {}
 _MIN_WS = 4 << 20
@@ -159,25 +161,84 @@ def _zeroed(size: int, dev: torch.device) -> torch.Tensor:
 def _workspace(lib, dev: torch.device, stream: int, m: int, ns: tuple, k: int, swiglu: bool, norm: bool = False):
     need = _ws_need(m, ns, k, bool(swiglu), bool(norm))
     if need == 0:
-        return ctypes.c_void_p(0), 0
+        return ctypes.c_void_p(0), 0, None
     key = (dev.index, stream)
     capturing, cid = _native.capture_state(stream)
-    if capturing:
-        cur = _capture_ws.get(key)
-        if cur is None or cur[0] != cid or cur[1].numel() < need:
-            grow = 2 * cur[1].numel() if cur is not None and cur[0] == cid else 0
-            _capture_ws[key] = (cid, _zeroed(max(need, grow, _MIN_WS), dev))
-        ws = _capture_ws[key][1]
-    else:
-        _capture_ws.pop(key, None)  # that capture is over
-        ws = _eager_ws.get(key)
-        if ws is None or ws.numel() < need:
-            ws = _zeroed(max(need, 2 * ws.numel() if ws is not None else 0, _MIN_WS), dev)
-            _eager_ws[key] = ws
-            while len(_eager_ws) > _MAX_EAGER_WS:
-                _eager_ws.popitem(last=False)
-        _eager_ws.move_to_end(key)
-    return ctypes.c_void_p(ws.data_ptr()), ws.numel()
+    with _ws_lock:
+        if capturing:
+            cur = _capture_ws.get(key)
+            if cur is None or cur[0] != cid or cur[1].numel() < need:
+                grow = 2 * cur[1].numel() if cur is not None and cur[0] == cid else 0
+                _capture_ws[key] = (cid, _zeroed(max(need, grow, _MIN_WS), dev))
+            ws = _capture_ws[key][1]
+        else:
+            _capture_ws.pop(key, None)  # that capture is over
+            ws = _eager_ws.get(key)
+            if ws is None or ws.numel() < need:
+                ws = _zeroed(max(need, 2 * ws.numel() if ws is not None else 0, _MIN_WS), dev)
+                _eager_ws[key] = ws
+                while len(_eager_ws) > _MAX_EAGER_WS:
+                    _eager_ws.popitem(last=False)
+            _eager_ws.move_to_end(key)
+    # the caller keeps the tensor until its launch is enqueued: a thread that
+    # replaces the buffer meanwhile cannot free it under that launch
+    return ctypes.c_void_p(ws.data_ptr()), ws.numel(), ws
+
+
+# ---------------------------------------------------------------------------
+# CPU-resident tensors: the reference formula in torch, on the CPU
+# ---------------------------------------------------------------------------
+# Used only for tensors that live on the CPU; GPU tensors never reach these.
+
+def _cpu_quantize(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """engine/quantization.py:20-22 in torch on the CPU: per-row absmax of the
+    fp32 weight floored at 1e-8, divided by 127 (IEEE fp32 divide), then
+    w / scale rounded half to even and clamped to +-127."""
+    w = weight.float()
+    scale = w.abs().amax(dim=1, keepdim=True).clamp(min=1e-8) / 127.0
+    return (w / scale).round().clamp(-127, 127).to(torch.int8), scale
+
+
+def _cpu_dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """engine/quantization.py:27: the fp32 product q * scale, then the cast."""
+    return (q.to(torch.float32) * scale.to(torch.float32).reshape(-1, 1)).to(dtype)
+
+
+def _tiles(n: int, k: int) -> tuple[int, int]:
+    return -(-n // 16), -(-k // 64)
+
+
+def _cpu_pack(q: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 [n, k] -> packed bytes (layout of :func:`packed_numel`)."""
+    n, k = q.shape
+    if n == 0 or k == 0:
+        return torch.empty(0, dtype=torch.int8)
+    tn, tk = _tiles(n, k)
+    padded = torch.zeros((tn * 16, tk * 64), dtype=torch.int8)
+    padded[:n, :k] = q
+    # [tile row, row, tile col, 16-column group, byte] -> [tile row, tile col, group, row, byte]
+    return padded.view(tn, 16, tk, 4, 16).permute(0, 2, 3, 1, 4).reshape(-1)
+
+
+def _cpu_tiles_to(qp: torch.Tensor, n: int, k: int, dtype: torch.dtype) -> torch.Tensor:
+    """Packed bytes -> the row-major [n, k] matrix in ``dtype``, converted in
+    the same pass as the reordering."""
+    if n == 0 or k == 0:
+        return torch.empty((n, k), dtype=dtype)
+    tn, tk = _tiles(n, k)
+    out = torch.empty((tn, 16, tk, 4, 16), dtype=dtype)
+    out.copy_(qp.view(tn, tk, 4, 16, 16).permute(0, 3, 1, 2, 4))
+    return out.view(tn * 16, tk * 64)[:n, :k]
+
+
+def _cpu_unpack(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    return _cpu_tiles_to(qp, n, k, torch.int8).contiguous()
+
+
+def _cpu_dequantize_packed(qp: torch.Tensor, scale: torch.Tensor, n: int, k: int,
+                           dtype: torch.dtype) -> torch.Tensor:
+    # the same fp32 products as _cpu_dequantize of the unpacked q
+    return (_cpu_tiles_to(qp, n, k, torch.float32) * scale.to(torch.float32).reshape(-1, 1)).to(dtype)
 
 
 # ---------------------------------------------------------------------------
@@ -197,13 +258,14 @@ def quantize_per_channel(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tens
     if k == 0 and n > 0:
         # torch's amax refuses an empty reduction dimension; so does the reference
         raise RuntimeError("amax(): Expected reduction dim 1 to have non-zero size.")
-    home = weight.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if weight.device.type != "cuda":
+        return _cpu_quantize(weight)
+    dev = weight.device
     lib = _native.load()
     w = weight
     if w.dtype not in (torch.float32, torch.bfloat16):
         w = w.float()  # the reference's own first step, weight.float()
-    w = _aligned(w.to(dev, non_blocking=False))
+    w = _aligned(w)
     q = torch.empty((n, k), dtype=torch.int8, device=dev)
     scale = torch.empty((n, 1), dtype=torch.float32, device=dev)
     with _on_device(dev):
@@ -211,8 +273,6 @@ def quantize_per_channel(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tens
             _ptr(w), _DTYPE_CODE[w.dtype], n, k, _ptr(q), _ptr(scale), _stream(dev)
         )
     check(rc, "quantize_per_channel")
-    if home.type != "cuda":
-        q, scale = q.to(home), scale.to(home)
     return q, scale
 
 
@@ -225,11 +285,12 @@ def dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torc
     n, k = q.shape
     if scale.numel() != n:
         raise ValueError(f"scale must hold one value per row ({n}), got shape {tuple(scale.shape)}")
-    home = q.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if q.device.type != "cuda":
+        return _cpu_dequantize(q, scale.to(q.device), dtype)
+    dev = q.device
     lib = _native.load()
     kdt = dtype if dtype in _DTYPE_CODE else torch.float32
-    qd = _aligned(q.to(dev))
+    qd = _aligned(q)
     sd = _aligned(scale.to(dev, dtype=torch.float32).reshape(n))
     out = torch.empty((n, k), dtype=kdt, device=dev)
     with _on_device(dev):
@@ -237,7 +298,7 @@ def dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torc
     check(rc, "dequantize")
     if kdt != dtype:
         out = out.to(dtype)  # fp32 product, then the reference's .to(dtype)
-    return out.to(home) if home.type != "cuda" else out
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -249,13 +310,16 @@ def _packed_numel(lib, n: int, k: int) -> int:
 
 
 def _quantize_packed(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """quantize_per_channel with q written in the packed layout, on the GPU."""
+    """quantize_per_channel with q written in the packed layout (on the
+    weight's device)."""
     n, k = weight.shape
-    home = weight.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if weight.device.type != "cuda":
+        q, scale = _cpu_quantize(weight)
+        return _cpu_pack(q), scale
+    dev = weight.device
     lib = _native.load()
     w = weight if weight.dtype in (torch.float32, torch.bfloat16) else weight.float()
-    w = _aligned(w.to(dev, non_blocking=False))
+    w = _aligned(w)
     qp = torch.empty(_packed_numel(lib, n, k), dtype=torch.int8, device=dev)
     scale = torch.empty((n, 1), dtype=torch.float32, device=dev)
     with _on_device(dev):
@@ -270,38 +334,41 @@ def pack(q: torch.Tensor) -> torch.Tensor:
     if q.dim() != 2 or q.dtype != torch.int8:
         raise ValueError("q must be a 2-D int8 tensor")
     n, k = q.shape
-    home = q.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if q.device.type != "cuda":
+        return _cpu_pack(q)
+    dev = q.device
     lib = _native.load()
-    qd = _aligned(q.to(dev))
+    qd = _aligned(q)
     qp = torch.empty(_packed_numel(lib, n, k), dtype=torch.int8, device=dev)
     with _on_device(dev):
         rc = lib.pgs_pack_weight(_ptr(qd), n, k, _ptr(qp), _stream(dev))
     check(rc, "pack")
-    return qp.to(home) if home.type != "cuda" else qp
+    return qp
 
 
 def unpack(qp: torch.Tensor, n: int, k: int) -> torch.Tensor:
     """The packed layout -> row-major int8 [N, K] (same device as ``qp``)."""
-    home = qp.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if qp.numel() != packed_numel(n, k):
+        raise ValueError(f"packed buffer holds {qp.numel()} bytes, [{n}, {k}] needs {packed_numel(n, k)}")
+    if qp.device.type != "cuda":
+        return _cpu_unpack(qp, n, k)
+    dev = qp.device
     lib = _native.load()
-    if qp.numel() != _packed_numel(lib, n, k):
-        raise ValueError(f"packed buffer holds {qp.numel()} bytes, [{n}, {k}] needs {_packed_numel(lib, n, k)}")
-    qd = _aligned(qp.to(dev))
+    qd = _aligned(qp)
     q = torch.empty((n, k), dtype=torch.int8, device=dev)
     with _on_device(dev):
         rc = lib.pgs_unpack_weight(_ptr(qd), n, k, _ptr(q), _stream(dev))
     check(rc, "unpack")
-    return q.to(home) if home.type != "cuda" else q
+    return q
 
 
 def _dequantize_packed(qp: torch.Tensor, scale: torch.Tensor, n: int, k: int, dtype: torch.dtype) -> torch.Tensor:
-    home = qp.device
-    dev = home if home.type == "cuda" else _require_gpu()
+    if qp.device.type != "cuda":
+        return _cpu_dequantize_packed(qp, scale.to(qp.device), n, k, dtype)
+    dev = qp.device
     lib = _native.load()
     kdt = dtype if dtype in _DTYPE_CODE else torch.float32
-    qd = _aligned(qp.to(dev))
+    qd = _aligned(qp)
     sd = _aligned(scale.to(dev, dtype=torch.float32).reshape(n))
     out = torch.empty((n, k), dtype=kdt, device=dev)
     with _on_device(dev):
@@ -309,23 +376,24 @@ def _dequantize_packed(qp: torch.Tensor, scale: torch.Tensor, n: int, k: int, dt
     check(rc, "dequantize")
     if kdt != dtype:
         out = out.to(dtype)
-    return out.to(home) if home.type != "cuda" else out
+    return out
 
 
 # ---------------------------------------------------------------------------
 # fused linears
 # ---------------------------------------------------------------------------
 
-def _ws_args(dev: torch.device, x, k: int, ns: tuple, swiglu: bool, norm: bool) -> tuple[int, int]:
-    """(pointer, bytes) of the K-split workspace a call needs, (0, 0) when its
-    plan splits nothing (every decode projection of a 2048-hidden model)."""
+def _ws_args(dev: torch.device, x, k: int, ns: tuple, swiglu: bool, norm: bool) -> tuple:
+    """(pointer, bytes, buffer) of the K-split workspace a call needs, (0, 0,
+    None) when its plan splits nothing (every decode projection of a
+    2048-hidden model).  Hold ``buffer`` until the launch is enqueued."""
     m = x.numel() // k if isinstance(x, torch.Tensor) and k else 0
     if m <= 0 or _ws_need(m, ns, k, swiglu, norm) == 0:
-        return 0, 0
+        return 0, 0, None
     lib = _native.load()
     with _on_device(dev):
-        ws, nbytes = _workspace(lib, dev, _raw_stream(dev), m, ns, k, swiglu, norm)
-    return ws.value or 0, nbytes
+        ws, nbytes, buf = _workspace(lib, dev, _raw_stream(dev), m, ns, k, swiglu, norm)
+    return ws.value or 0, nbytes, buf
 
 
 def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None = None,
@@ -347,7 +415,7 @@ def linear(x: torch.Tensor, weight: "QuantizedWeight", bias: torch.Tensor | None
     if not weight.qp.is_cuda:
         raise RuntimeError("W8A16 linear: the weight must be on a ROCm GPU (call .to('cuda') first)")
     q, s, n, k, dev = weight._launch_operands()
-    ws, ws_bytes = _ws_args(dev, x, k, (n,), False, False)
+    ws, ws_bytes, _buf = _ws_args(dev, x, k, (n,), False, False)
     return _native.load_host().linear1(x, q, s, bias, n, k, out_dtype is torch.float32, residual, out, ws, ws_bytes)
 
 
@@ -514,7 +582,7 @@ def _linear_group(x, weights, biases, out_dtype, norm_weight, eps) -> list[torch
         if o[3] != k or o[4] != dev:
             raise ValueError("linear_group: weights must share device and in_features")
     qs, ss, ns = [o[0] for o in ops], [o[1] for o in ops], tuple(o[2] for o in ops)
-    ws, ws_bytes = _ws_args(dev, x, k, ns, False, norm_weight is not None)
+    ws, ws_bytes, _buf = _ws_args(dev, x, k, ns, False, norm_weight is not None)
     return _native.load_host().linear(x, qs, ss, biases, ns, k, out_dtype is torch.float32, None, None, norm_weight,
                                       eps, ws, ws_bytes)
 
@@ -542,7 +610,7 @@ def _swiglu(x, gate, up, norm_weight, eps) -> torch.Tensor:
         raise RuntimeError("swiglu: gate and up weights must be on the same ROCm GPU")
     if (n, k) != (nu, ku):
         raise ValueError("swiglu: gate and up weights must have the same shape")
-    ws, ws_bytes = _ws_args(dev, x, k, (n,), True, norm_weight is not None)
+    ws, ws_bytes, _buf = _ws_args(dev, x, k, (n,), True, norm_weight is not None)
     return _native.load_host().swiglu(x, qg, sg, qu, su, n, k, norm_weight, eps, ws, ws_bytes)
 
 
@@ -585,10 +653,7 @@ class QuantizedWeight:
             raise RuntimeError("amax(): Expected reduction dim 1 to have non-zero size.")
         self.dtype = weight.dtype
         self.shape = torch.Size(weight.shape)
-        qp, scale = _quantize_packed(weight)
-        if weight.device.type != "cuda":
-            qp, scale = qp.to(weight.device), scale.to(weight.device)
-        self.qp, self.scale = qp, scale
+        self.qp, self.scale = _quantize_packed(weight)
 
     @property
     def q(self) -> torch.Tensor:
@@ -613,7 +678,7 @@ class QuantizedWeight:
                 v = (self.qp, self.scale, W8A16Weight(self))
                 self._view = v
             return v[2]
-        return self.dense()
+        return self.dense()  # a CPU weight: the reference's dequantized tensor, computed on the CPU
 
     def to(self, device) -> "QuantizedWeight":
         self.qp = self.qp.to(device)

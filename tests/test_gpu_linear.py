@@ -310,6 +310,48 @@ def test_calls_from_a_worker_thread(gpu):
     assert torch.equal(out["g"], Q.swiglu(xt, qw, qw))
 
 
+def test_split_plans_from_concurrent_threads(gpu):
+    """Four threads, each on its own stream, run K-split plans (each needs a
+    workspace: one per stream, made on first use, some grown later) at the
+    same time as the main thread: every result equals the single-threaded
+    one bit for bit."""
+    import threading
+
+    cases = [_problem(gpu, 70 + j, m, n, k) for j, (m, n, k) in
+             enumerate([(200, 2048, 11008), (64, 2048, 11008), (12, 2048, 11008), (600, 2048, 11008)])]
+    xs = [bf16_gpu(c[3], gpu) for c in cases]
+    want = [c[0].linear(x) for c, x in zip(cases, xs)]
+    torch.cuda.synchronize()
+    got, errs = {}, []
+    start = threading.Barrier(5)
+
+    def work(t):
+        try:
+            side = torch.cuda.Stream(device=gpu)
+            start.wait(30)
+            with torch.cuda.stream(side):
+                for rep in range(6):
+                    j = (t + rep) % len(cases)
+                    got[(t, rep)] = (j, cases[j][0].linear(xs[j]))
+            side.synchronize()
+        except BaseException as e:  # reported in the main thread
+            errs.append(e)
+
+    threads = [threading.Thread(target=work, args=(t,), daemon=True) for t in range(4)]
+    for t in threads:
+        t.start()
+    start.wait(30)
+    main = [c[0].linear(x) for c, x in zip(cases, xs)]
+    for t in threads:
+        t.join(120)
+    torch.cuda.synchronize()
+    assert not any(t.is_alive() for t in threads) and not errs, errs
+    assert all(torch.equal(a, b) for a, b in zip(main, want))
+    assert len(got) == 24
+    for (t, rep), (j, y) in got.items():
+        assert torch.equal(y, want[j]), (t, rep, j)
+
+
 def _plan_kernel() -> str:
     from pageserve_amd import _native
 

@@ -75,12 +75,21 @@ def test_misaligned_view_takes_the_scalar_path(gpu):
     _assert_bit_exact(q.cpu().numpy(), s.cpu().numpy(), q_ref, s_ref, "misaligned")
 
 
-def test_cpu_weight_round_trips_through_the_gpu(gpu):
+def test_cpu_and_gpu_weights_quantize_alike(gpu):
+    """A CPU weight is quantized by torch on the CPU, a GPU one by the HIP
+    kernel: the same bytes either way, and a weight moved between them keeps
+    them."""
     w = weights(8, 96, 256)
     q, s = Q.quantize_per_channel(torch.from_numpy(w))
     assert q.device.type == "cpu" and s.device.type == "cpu"
     q_ref, s_ref = O.quantize_per_channel(w)
     _assert_bit_exact(q.numpy(), s.numpy(), q_ref, s_ref, "cpu-resident weight")
+    qg, sg = Q.quantize_per_channel(torch.from_numpy(w).to(gpu))
+    assert torch.equal(qg.cpu(), q) and torch.equal(sg.cpu(), s)
+    qw = Q.QuantizedWeight(torch.from_numpy(w).to(torch.bfloat16))
+    dense_cpu = qw.get()
+    assert qw.to(gpu) is qw and torch.equal(qw.dense().cpu(), dense_cpu)
+    assert torch.equal(qw.to("cpu").get(), dense_cpu)
 
 
 def test_lm_head_shape_full_size(gpu):

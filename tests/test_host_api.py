@@ -32,14 +32,14 @@ def test_product_never_imports_the_oracle():
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU behaviour")
-def test_no_gpu_means_an_error_not_a_fallback():
-    w = torch.randn(8, 16)
-    with pytest.raises(RuntimeError, match="no ROCm GPU"):
-        Q.quantize_per_channel(w)
-    with pytest.raises(RuntimeError, match="no ROCm GPU"):
-        Q.QuantizedWeight(w)
-    with pytest.raises(RuntimeError, match="no ROCm GPU"):
-        Q.dequantize(torch.zeros(2, 16, dtype=torch.int8), torch.ones(2, 1), torch.float32)
+def test_no_gpu_fused_path_is_an_error_not_a_fallback():
+    """Without a GPU the fused linears raise; only CPU tensors' own reference
+    math (quantize, dequantize, get) runs on the CPU."""
+    qw = Q.QuantizedWeight(torch.randn(8, 16))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        Q.linear(torch.zeros(1, 16, dtype=torch.bfloat16), qw)
+    with pytest.raises(RuntimeError):
+        qw.to("cuda")
 
 
 def test_shape_errors_match_reference_behaviour():
