@@ -317,6 +317,95 @@ def decode_chain(layers, x0, attn, norms, rope, m):
     return step, nbytes, launches, single
 
 
+def chain_operands(dev, n_layers, m):
+    """Per layer (input norm, post-attention norm) weights ~ 1 + N(0, 0.1),
+    and the rotary rows of the reference's cache (engine/model.py:42-47) at
+    one position per token (positions 4096..)."""
+    ng = torch.Generator(device=dev).manual_seed(77)
+    norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
+                   for _ in range(2)) for _ in range(n_layers)]
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, device=dev).float() / 128))
+    emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
+    return norms, (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
+
+
+def span_timeline(dev, layers_n, m, command):
+    """Stage timeline of the single-launch decode chain: per-workgroup
+    timestamps of every stage boundary (pageserve_amd.span tracing), from a
+    graph of the chain captured with tracing on and replayed; returns a
+    markdown summary.  Times are relative to the launch's first workgroup
+    start, in microseconds (the trace clock runs at 100 MHz)."""
+    import statistics
+
+    from pageserve_amd import span as S
+
+    layers = make_layers(dev, layers_n)
+    gen = torch.Generator(device=dev).manual_seed(99 + m)
+    x = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    xo = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    norms, rope = chain_operands(dev, layers_n, m)
+    step, _, _, single = decode_chain(layers, x, xo, norms, rope, m)
+    if not single:
+        raise SystemExit(f"bench.py: no single-launch decode span at m={m}")
+    plain, _ = capture(step)
+    plain_ms = time_graph(plain, 50, 10)
+    del plain
+    slots = 64
+    buf = torch.zeros(slots * 256 * 16, dtype=torch.int64, device=dev)
+    S.decode_span_trace(buf)
+    try:
+        traced, _ = capture(step)  # the launches capture the trace pointer
+        traced_ms = time_graph(traced, 50, 10)
+        buf.zero_()
+        traced.replay()
+        torch.cuda.synchronize()
+        del traced
+    finally:
+        S.decode_span_trace(None)
+    tr = buf.view(slots, 256, 16).cpu()
+    # each replay's workspace starts from a cleared epoch: launch i carries tag i + 1
+    launches = [tr[(i + 1) % slots] for i in range(layers_n)]
+    names = S.TRACE_MARKS
+    full = launches[:-1]  # the last layer ends after publishing x2 (no next q|k|v)
+    rows = []
+    for i in range(1, 13):
+        p50s, maxs, durs = [], [], []
+        for t in full:
+            t0 = int(t[:, 0].min())
+            rel = (t[:, i].double() - t0) / 100.0  # us
+            prev = (t[:, i - 1].double() - t0) / 100.0
+            p50s.append(float(rel.median()))
+            maxs.append(float(rel.max()))
+            durs.append(float((rel - prev).median()))
+        rows.append((names[i], statistics.median(durs), statistics.median(p50s), statistics.median(maxs)))
+    spans = [(int(t[:, 12].max()) - int(t[:, 0].min())) / 100.0 for t in full]
+    starts = [(int(t[:, 0].max()) - int(t[:, 0].min())) / 100.0 for t in full]
+    gaps = [(int(launches[i + 1][:, 0].min()) - int(launches[i][:, 12].max())) / 100.0 for i in range(layers_n - 2)]
+    polls = [[int(v) for v in t[:, 13 + g]] for g in range(3) for t in launches]
+    poll_med = [statistics.median([statistics.median(p) for p in polls[g * layers_n:(g + 1) * layers_n]])
+                for g in range(3)]
+    lines = [f"# Decode span stage timeline, M={m}, Qwen2.5-3B ({layers_n} layers, one persistent launch per layer)",
+             "", "Command (repository root):", "", "```", command, "```", "",
+             "Per-workgroup timestamps (`s_memrealtime`, 100 MHz) written by lane 0 of each workgroup's control wave "
+             "at every stage boundary of `span_kernel` (tracing on: `pgs_w8a16_decode_span_trace`), from one replay "
+             "of a HIP graph of the whole chain. Times in microseconds from the launch's first workgroup start; "
+             "each figure is the median over the launches of layers 0.."
+             f"{layers_n - 2} (the last layer's launch has no q|k|v stage).", "",
+             f"- graph replay of the chain: {plain_ms * 1e3:.1f} us untraced, {traced_ms * 1e3:.1f} us traced "
+             f"({plain_ms * 1e3 / layers_n:.2f} / {traced_ms * 1e3 / layers_n:.2f} us per layer)",
+             f"- launch span (first start to last end): median {statistics.median(spans):.2f} us, "
+             f"min {min(spans):.2f}, max {max(spans):.2f}",
+             f"- spread of the 256 workgroup starts: median {statistics.median(starts):.2f} us",
+             f"- gap from a launch's last end to the next one's first start: median {statistics.median(gaps):.2f} us",
+             f"- polls per workgroup before each gather saw every word (median): x1 {poll_med[0]:.0f}, act "
+             f"{poll_med[1]:.0f}, x2 {poll_med[2]:.0f}", "",
+             "| stage boundary | phase us (p50 over workgroups) | at us, p50 workgroup | at us, last workgroup |",
+             "|---|---:|---:|---:|"]
+    for name, d, a, b in rows:
+        lines.append(f"| {name} | {d:.2f} | {a:.2f} | {b:.2f} |")
+    return "\n".join(lines) + "\n"
+
+
 def capture(fn):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -922,6 +1011,8 @@ def main():
                     help="run only the dispatches the rocprofv3 --pmc traffic passes read")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="reduce rocprofv3 --pmc output directories to the traffic summary (no GPU)")
+    ap.add_argument("--span-timeline", metavar="OUT",
+                    help="write the single-launch decode chain's stage timeline (markdown) to OUT and exit")
     ap.add_argument("--prefill-workload", type=int, metavar="M",
                     help="run only the prefill sweep's launches once per layer at M tokens (counter passes)")
     ap.add_argument("--plan-file", default="gpurun_out/prefill_plans.json",
@@ -967,6 +1058,14 @@ def main():
         with torch.inference_mode():
             pmc_workload(dev, args.layers)
         return
+    if args.span_timeline:
+        os.makedirs(os.path.dirname(os.path.abspath(args.span_timeline)), exist_ok=True)
+        with torch.inference_mode():
+            md = span_timeline(dev, args.layers, args.m, "python3 bench.py " + " ".join(sys.argv[1:]))
+        with open(args.span_timeline, "w") as f:
+            f.write(md)
+        log(f"[bench] span timeline written to {args.span_timeline}")
+        return
     if args.prefill_workload:
         os.makedirs(os.path.dirname(os.path.abspath(args.plan_file)), exist_ok=True)
         with torch.inference_mode():
@@ -986,14 +1085,7 @@ def main():
         xi = torch.randn((m, INTER), generator=gen, device=dev).to(torch.bfloat16)
         if args.only in ("all", "decode"):
             gate_inputs[m] = (x, xo)
-            # norm weights and the rotary rows of the reference's cache
-            # (engine/model.py:42-47) at one position per token
-            ng = torch.Generator(device=dev).manual_seed(77)
-            norms = [tuple((1 + 0.1 * torch.randn(HIDDEN, generator=ng, device=dev)).to(torch.bfloat16)
-                           for _ in range(2)) for _ in layers]
-            inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, device=dev).float() / 128))
-            emb = torch.cat((torch.outer(torch.arange(4096, 4096 + m, device=dev).float(), inv_freq),) * 2, dim=-1)
-            rope = (emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16))
+            norms, rope = chain_operands(dev, len(layers), m)
             gate_inputs["span"] = (norms, rope, x, xo)
             # the headline: the dependent decode chain
             step, nbytes, launches, single = decode_chain(layers, x, xo, norms, rope, m)

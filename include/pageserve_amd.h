@@ -409,6 +409,22 @@ int pgs_w8a16_decode_span_status(void* workspace, int reset, void* stream);
  */
 int pgs_w8a16_decode_span_test_hooks(int spin_limit, int force_giveup);
 
+/*
+ * Tracing aid, no counterpart in the reference: with a device buffer set,
+ * every later decode span launch writes per-workgroup stage timestamps
+ * (s_memrealtime, a constant 100 MHz clock) into it, laid out
+ * [slots][256 workgroups][16] uint64 with slots = bytes / 32768 (at most
+ * 65535) and slot = launch tag % slots (the tag advances by one per launch
+ * on a workspace).  Entries 0..12: launch start, end of the prologue, end of
+ * o_proj's stream, o_proj's result published, x1 gathered (RMSNorm done),
+ * end of gate|up's stream, activations published, activations gathered,
+ * end of down_proj's stream, x2 published, x2 gathered (next RMSNorm done),
+ * end of q|k|v's stream, end of the launch; 13..15: polls of the three
+ * gathers.  NULL turns it off.  Process-wide; the buffer must outlive the
+ * launches that write it.
+ */
+int pgs_w8a16_decode_span_trace(void* buffer, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

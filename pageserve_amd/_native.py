@@ -23,7 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 OK = 0
 MAX_GROUP = 4
-ABI_VERSION = 9
+ABI_VERSION = 10
 ERR_TIMEOUT = 5
 
 
@@ -110,6 +110,7 @@ SIGNATURES = {
     "pgs_w8a16_decode_span_supported": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "pgs_w8a16_decode_span_status": (_INT, [_VP, _INT, _VP]),
     "pgs_w8a16_decode_span_test_hooks": (_INT, [_INT, _INT]),
+    "pgs_w8a16_decode_span_trace": (_INT, [_VP, _SZ]),
 }
 
 _lock = threading.Lock()

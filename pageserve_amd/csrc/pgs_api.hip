@@ -85,7 +85,7 @@ void note_launch(const char* kernel, long long grid, int splits, const char* sec
 
 extern "C" {
 
-int pgs_abi_version(void) { return 9; }
+int pgs_abi_version(void) { return 10; }
 
 const char* pgs_error_string(int code) {
   switch (code) {

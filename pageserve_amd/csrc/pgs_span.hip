@@ -58,14 +58,20 @@
 
 #include "pgs_linear.h"
 
-// Phase marks for tuning builds (a timing harness defines PGS_SPAN_MARK to
-// record a timestamp per workgroup and phase); nothing by default.
-#ifndef PGS_SPAN_MARK
-#define PGS_SPAN_MARK(i)
-#endif
-#ifndef PGS_SPAN_NOTE
-#define PGS_SPAN_NOTE(i, v)
-#endif
+// Stage timestamps (a tracing aid).  With a trace buffer set
+// (pgs_w8a16_decode_span_trace), lane 0 of each workgroup's control wave
+// writes s_memrealtime (a constant 100 MHz clock) at every stage boundary
+// into slot (launch tag % slots) of the buffer, laid out [slots][256
+// workgroups][16] u64: entries 0..12 the marks below, 13..15 the poll
+// counts of the three gathers.  Without one, a mark is a uniform branch.
+#define PGS_SPAN_MARK(i)                                                    \
+  do {                                                                      \
+    if (tracing && tid == kSpanSW * 64) trow[i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define PGS_SPAN_NOTE(i, v)                                   \
+  do {                                                        \
+    if (tracing && tid == kSpanSW * 64) trow[i] = (v);        \
+  } while (0)
 
 namespace pgs {
 namespace {
@@ -178,6 +184,8 @@ struct SpanParams {
   float eps;
   int spin_limit;
   int force_giveup;
+  unsigned long long* trace;  // null: no stage timestamps
+  int trace_slots;
 };
 
 // Where a unit's weights are: its 16-row block row (whole K) and the byte
@@ -542,7 +550,9 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     return false;
   };
 
-  PGS_SPAN_MARK(0);
+  const bool tracing = p.trace != nullptr;
+  const unsigned long long t_start = tracing ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  unsigned long long* trow = p.trace;  // this workgroup's row, once the tag is known
   // ================= prologue =================
   // The control wave's operand loads and the streaming waves' o_proj weight
   // loads go out together (o_proj is 16 KiB per CU; the deeper weight
@@ -637,6 +647,8 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   }
   barrier_lds();
   if (abort_now()) return;
+  if (tracing) trow = p.trace + (static_cast<int64_t>(static_cast<uint32_t>(flag[1]) % p.trace_slots) * kSpanG + wg) * 16;
+  PGS_SPAN_NOTE(0, t_start);
   PGS_SPAN_MARK(1);
 
   // ================= stage 0: o_proj + residual =================
@@ -799,6 +811,8 @@ int launch_span(const SpanParams& p, hipStream_t st, int dev) {
 
 int g_spin_limit = 1 << 18;
 int g_force_giveup = 0;
+unsigned long long* g_trace = nullptr;
+int g_trace_slots = 0;
 
 }  // namespace
 }  // namespace pgs
@@ -822,6 +836,22 @@ extern "C" int pgs_w8a16_decode_span_test_hooks(int spin_limit, int force_giveup
   if (spin_limit < 0) return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_w8a16_decode_span_test_hooks: negative spin limit");
   g_spin_limit = spin_limit == 0 ? (1 << 18) : spin_limit;
   g_force_giveup = force_giveup ? 1 : 0;
+  return PGS_OK;
+}
+
+extern "C" int pgs_w8a16_decode_span_trace(void* buffer, size_t bytes) {
+  constexpr size_t kSlotBytes = static_cast<size_t>(kSpanG) * 16 * sizeof(unsigned long long);
+  if (!buffer) {
+    g_trace = nullptr;
+    g_trace_slots = 0;
+    return PGS_OK;
+  }
+  if (!aligned(buffer, 8) || bytes < kSlotBytes)
+    return fail(PGS_ERR_INVALID_ARGUMENT, "pgs_w8a16_decode_span_trace: need an 8-byte aligned buffer of at least %zu bytes",
+                kSlotBytes);
+  const size_t slots = bytes / kSlotBytes;
+  g_trace = static_cast<unsigned long long*>(buffer);
+  g_trace_slots = static_cast<int>(slots > 65535 ? 65535 : slots);
   return PGS_OK;
 }
 
@@ -904,6 +934,8 @@ extern "C" int pgs_w8a16_decode_span(const void* attn, const void* residual, voi
   p.eps = eps;
   p.spin_limit = g_spin_limit;
   p.force_giveup = g_force_giveup;
+  p.trace = g_trace;
+  p.trace_slots = g_trace_slots;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (int rc = require_device(fn, st)) return rc;
   int dev = -1;

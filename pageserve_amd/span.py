@@ -27,7 +27,7 @@ from . import _native
 from . import quantization as Q
 from ._native import LinearOut, SpanNext, SpanWeights, check
 
-__all__ = ["decode_span", "decode_span_status", "span_supported"]
+__all__ = ["decode_span", "decode_span_status", "decode_span_trace", "span_supported", "TRACE_MARKS"]
 
 # Workspaces of the persistent launch (epoch, error word and exchange
 # buffers; zero before first use): one per (device, stream) for eager calls,
@@ -75,6 +75,34 @@ def decode_span_status(device: torch.device | None = None, reset: bool = True) -
     with Q._on_device(dev):
         rc = lib.pgs_w8a16_decode_span_status(ctypes.c_void_p(ws.data_ptr()), int(reset), ctypes.c_void_p(stream))
     check(rc, "decode_span")
+
+
+# stage names of the 13 timestamps a traced launch writes per workgroup
+TRACE_MARKS = ("start", "prologue", "o streamed", "x1 published", "x1 gathered + norm", "gate|up streamed",
+               "act published", "act gathered", "down streamed", "x2 published", "x2 gathered + norm",
+               "q|k|v streamed", "end")
+_trace_buf: torch.Tensor | None = None
+
+
+def decode_span_trace(buffer: torch.Tensor | None) -> None:
+    """Turns stage tracing of the single-launch span on (``buffer``: a
+    contiguous int64 CUDA tensor of ``slots * 256 * 16`` entries) or off
+    (None).  While on, each launch writes per-workgroup timestamps (100 MHz
+    ticks) into ``buffer.view(slots, 256, 16)[tag % slots]``: entries 0..12
+    the :data:`TRACE_MARKS`, 13..15 the poll counts of the three gathers.
+    The buffer is kept referenced until tracing is turned off."""
+    global _trace_buf
+    lib = _native.load()
+    if buffer is None:
+        check(lib.pgs_w8a16_decode_span_trace(None, 0), "decode_span_trace")
+        _trace_buf = None
+        return
+    if (not isinstance(buffer, torch.Tensor) or not buffer.is_cuda or buffer.dtype != torch.int64
+            or not buffer.is_contiguous() or buffer.numel() % (256 * 16) or buffer.numel() == 0):
+        raise ValueError("decode_span_trace: buffer must be a contiguous int64 CUDA tensor of slots * 4096 entries")
+    check(lib.pgs_w8a16_decode_span_trace(ctypes.c_void_p(buffer.data_ptr()), buffer.numel() * 8),
+          "decode_span_trace")
+    _trace_buf = buffer
 
 
 def _bf16_vec(t: torch.Tensor, n: int, dev, name: str) -> torch.Tensor:

@@ -187,6 +187,50 @@ def test_span_repeats_and_graph_replays_are_bit_equal(gpu, layer):
     S.decode_span_status(gpu)
 
 
+def test_span_trace_records_every_stage_and_changes_nothing(gpu, layer):
+    """Tracing on: the outputs equal an untraced launch's bit for bit; each
+    of the 256 workgroups of each launch writes its 13 marks into the slot
+    of the launch's tag, non-decreasing, and the poll counts; a launch with
+    the next layer's q|k|v reaches the last mark, one without stops after
+    the x2 mark.  Bad buffers are refused; off again, nothing is written."""
+    m = 1
+    x, attn = activations(380, m, H), activations(381, m, H)
+    xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
+    cos, sin = (bf16_gpu(t, gpu) for t in rope_tables(m))
+    ref = [t.clone() for t in (lambda r: [r[0], *r[1]])(run_span(layer, at, xt, cos, sin))]
+    torch.cuda.synchronize()
+    slots = 4
+    buf = torch.zeros(slots * 256 * 16, dtype=torch.int64, device=gpu)
+    with pytest.raises(ValueError):
+        S.decode_span_trace(buf[:100])
+    with pytest.raises(ValueError):
+        S.decode_span_trace(buf.view(torch.float64))
+    S.decode_span_trace(buf)
+    try:
+        got, (q, k, v) = run_span(layer, at, xt, cos, sin)
+        last, _ = run_span(layer, at, xt, last=True)
+        torch.cuda.synchronize()
+    finally:
+        S.decode_span_trace(None)
+    for a, b in zip(ref, [got, q, k, v]):
+        assert torch.equal(a, b)
+    tr = buf.view(slots, 256, 16).cpu()
+    used = [i for i in range(slots) if tr[i, :, 0].ne(0).any()]
+    assert len(used) == 2 and (used[1] - used[0]) % slots in (1, slots - 1)
+    first, second = (used[0], used[1]) if (used[0] + 1) % slots == used[1] else (used[1], used[0])
+    full, tail = tr[first], tr[second]
+    assert bool((full[:, :13] > 0).all())
+    assert bool((full[:, 1:13] >= full[:, 0:12]).all())
+    assert bool((full[:, 13:16] >= 1).all())  # every gather polled at least once
+    assert bool((tail[:, :10] > 0).all()) and bool((tail[:, 10:13] == 0).all())
+    assert bool((tail[:, 1:10] >= tail[:, 0:9]).all())
+    buf.zero_()
+    run_span(layer, at, xt, cos, sin)
+    torch.cuda.synchronize()
+    assert not bool(buf.ne(0).any())
+    S.decode_span_status(gpu)
+
+
 def test_span_giveup_reports_timeout_and_recovers(gpu, layer, native_lib):
     """The bounded wait's give-up path, forced from the host (every gather
     waits for a tag no workgroup writes, two polls): the launch ends, the
