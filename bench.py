@@ -632,17 +632,16 @@ def kernel_pattern(plan: str) -> tuple[str, str | None]:
             "launch_cfg": "gemm_kernel", "launch_instance": "skinny_kernel"}[m.group(1)]
     reduce = None
     if "then gemm_reduce_kernel" in plan:
-        reduce = "gemm_reduce_kernel<" + ", ".join(vals[:4]) + ">"
+        reduce = "gemm_reduce_kernel<" + ", ".join(vals[:4])  # then the split count
     return f"{name}<{', '.join(vals)}>", reduce
 
 
-def mfma_summary(pmc_dir, plan_path, command):
-    """Per launch kind: mean dispatch duration (the counter pass's own
-    timestamps), MfmaUtil, MFMA flops counted by the hardware, and the
-    algorithmic TFLOP/s against the 2.5 PFLOP/s bf16 dense peak."""
+def _prefill_dispatches(pmc_dir, plan_path):
+    """(plan, [(kind, kernel pattern)], {kind: [dispatch rows]}) of a
+    --prefill-workload counter pass: every counter of each dispatch, keyed by
+    counter name, and its duration ("ns")."""
     import csv
     import glob
-    import statistics
 
     with open(plan_path) as f:
         plan = json.load(f)
@@ -654,7 +653,6 @@ def mfma_summary(pmc_dir, plan_path, command):
                                                                           "id": r["Dispatch_Id"]})
                 d[r["Counter_Name"]] = float(r["Counter_Value"])
                 d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-    m = plan["m"]
     # the workload issues, per layer, the launch kinds in PREFILL_KINDS order
     # (each followed by its reduce kernel when it has one): walk this
     # package's dispatches in dispatch order and hand each to the next
@@ -676,6 +674,17 @@ def mfma_summary(pmc_dir, plan_path, command):
                 by_kind[kind].append(d)
                 i = (i + step + 1) % len(seq)
                 break
+    return plan, seq, by_kind
+
+
+def mfma_summary(pmc_dir, plan_path, command):
+    """Per launch kind: mean dispatch duration (the counter pass's own
+    timestamps), MfmaUtil, MFMA flops counted by the hardware, and the
+    algorithmic TFLOP/s against the 2.5 PFLOP/s bf16 dense peak."""
+    import statistics
+
+    plan, seq, by_kind = _prefill_dispatches(pmc_dir, plan_path)
+    m = plan["m"]
     lines = [f"# MFMA utilisation of the prefill launches, M={m}, Qwen2.5-3B linears ({plan['layers']} layers)", "",
              "Command (repository root):", "", "```", command, "```", "",
              "Counters per dispatch from `rocprofv3 --pmc` (one pass: `MfmaUtil` = SQ_VALU_MFMA_BUSY_CYCLES summed "
@@ -699,6 +708,47 @@ def mfma_summary(pmc_dir, plan_path, command):
         tf = alg * 1e9 / (us * 1e-6) / 1e12 if alg else 0.0
         lines.append(f"| {kind} | `{pat}` | {len(ds)} | {us:.2f} | {util:.1f} | {hw:.2f} | {alg:.2f} | "
                      f"{tf:.1f} | {100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f} |")
+    return "\n".join(lines) + "\n"
+
+
+# what the counter table says about each counter it may find
+COUNTER_NOTES = {
+    "VALUBusy": "% of GPU time the CUs issue vector ALU instructions (100 SQ_ACTIVE_INST_VALU / CUs / GRBM_GUI_ACTIVE)",
+    "LdsUtil": "% of GPU time the LDS is active (100 SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE x CUs))",
+    "MfmaUtil": "% of SIMD cycles the MFMA unit is busy",
+    "SQ_LDS_BANK_CONFLICT": "cycles LDS is stalled by bank conflicts (sum over CUs)",
+    "SQ_INSTS_LDS": "LDS instructions issued (all waves)",
+    "SQ_INSTS_VALU": "vector ALU instructions issued, MFMAs included",
+    "SQ_INSTS_MFMA": "MFMA instructions issued",
+}
+
+
+def counter_summary(pmc_dir, plan_path, command):
+    """Per launch kind of a --prefill-workload counter pass: mean dispatch
+    duration and the mean of every counter the pass collected."""
+    import statistics
+
+    plan, seq, by_kind = _prefill_dispatches(pmc_dir, plan_path)
+    names = sorted({k for ds in by_kind.values() for d in ds for k in d if k not in ("name", "id", "ns")})
+    lines = [f"# Counters of the prefill launches, M={plan['m']}, Qwen2.5-3B linears ({plan['layers']} layers)", "",
+             "Command (repository root):", "", "```", command, "```", "",
+             "Counters per dispatch from one `rocprofv3 --pmc` pass, mean over the dispatches of each launch kind "
+             "(assigned in dispatch order: the workload issues q|k|v, o, gate|up, down per layer); durations from "
+             "the same pass's dispatch timestamps (kernels serialised by counter collection).", ""]
+    for n in names:
+        lines.append(f"- `{n}`: {COUNTER_NOTES.get(n, 'raw counter, summed over instances')}")
+    lines += ["", "| launch | kernel | dispatches | mean us | " + " | ".join(names) + " |",
+              "|---|---|---:|---:|" + "---:|" * len(names)]
+    for kind, pat in seq:
+        ds = by_kind[kind]
+        if not ds:
+            continue
+        us = statistics.mean(d["ns"] for d in ds) / 1e3
+        vals = []
+        for n in names:
+            v = statistics.mean(d.get(n, float("nan")) for d in ds)
+            vals.append(f"{v:.1f}" if abs(v) < 1e4 else f"{v:.4g}")
+        lines.append(f"| {kind} | `{pat}` | {len(ds)} | {us:.2f} | " + " | ".join(vals) + " |")
     return "\n".join(lines) + "\n"
 
 
@@ -1019,11 +1069,20 @@ def main():
                     help="where --prefill-workload records each launch kind's kernel instance")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "PLAN_FILE"),
                     help="reduce a rocprofv3 --pmc pass over --prefill-workload to an MFMA table (no GPU)")
-    ap.add_argument("--summary-out", help="file --mfma-summary writes (stdout too)")
+    ap.add_argument("--counter-summary", nargs=2, metavar=("PMC_DIR", "PLAN_FILE"),
+                    help="tabulate every counter of a --prefill-workload counter pass per launch kind (no GPU)")
+    ap.add_argument("--summary-out", help="file --mfma-summary / --counter-summary writes (stdout too)")
     ap.add_argument("--pmc-command", action="append", default=[],
                     help="command line recorded in the traffic summary (repeatable)")
     args = ap.parse_args()
 
+    if args.counter_summary:
+        text = counter_summary(args.counter_summary[0], args.counter_summary[1], " ".join(args.pmc_command))
+        if args.summary_out:
+            with open(args.summary_out, "w") as f:
+                f.write(text)
+        print(text, end="")
+        return
     if args.mfma_summary:
         text = mfma_summary(args.mfma_summary[0], args.mfma_summary[1], " ".join(args.pmc_command))
         if args.summary_out:

@@ -833,8 +833,12 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_dma_kernel(const uint16_t*
 
 // Sums the split partial tiles in split order and runs the epilogue.  One
 // thread per accumulator slot (4 consecutive output rows of one token) over
-// all tiles; partial reads are coalesced 16-byte loads.
-template <int BM, int BN, int NMAT, bool OUT_F32>
+// all tiles; partial reads are coalesced 16-byte loads.  With the split
+// count known (SPL = 2, 4, 8; 0: read at run time) every partial load is in
+// flight before the first add (a runtime loop waits for each in turn), and
+// the epilogue operands are requested before them; the sum is the same
+// ((0 + p0) + p1) + ... either way.
+template <int BM, int BN, int NMAT, bool OUT_F32, int SPL>
 __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
   constexpr int TM = BM / 16, TN = BN / 64;
   constexpr int SLOTS = 4 * TN * TM * 64;  // per tile and matrix
@@ -859,15 +863,45 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
   const int m = m0 + mt * 16 + (lane & 15);
   const int nb = n0 + wave * (BN / 4) + nt * 16 + 4 * (lane >> 4);
   if (m >= M) return;
+  const Rows4<NMAT> e = rows4<NMAT>(a, g, N, nb);
   const f32x4* part = reinterpret_cast<const f32x4*>(ga.partials) + static_cast<int64_t>(t) * ga.splits * NMAT * SLOTS;
   f32x4 v[NMAT];
+  if constexpr (SPL > 0) {
+    f32x4 pv[NMAT][SPL];
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat) {
-    v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < ga.splits; ++sp) v[mat] += part[(static_cast<int64_t>(sp) * NMAT + mat) * SLOTS + slot];
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int sp = 0; sp < SPL; ++sp) pv[mat][sp] = part[(sp * NMAT + mat) * SLOTS + slot];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < SPL; ++sp) v[mat] += pv[mat][sp];
+    }
+  } else {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < ga.splits; ++sp) v[mat] += part[(static_cast<int64_t>(sp) * NMAT + mat) * SLOTS + slot];
+    }
   }
   void* y = (NMAT == 2) ? a.y[0] : pick(a.y, g);
-  store_rows4<NMAT, OUT_F32>(a, g, N, m, nb, rows4<NMAT>(a, g, N, nb), v[0], v[NMAT - 1], y, vec_out<OUT_F32>(y, N));
+  store_rows4<NMAT, OUT_F32>(a, g, N, m, nb, e, v[0], v[NMAT - 1], y, vec_out<OUT_F32>(y, N));
+}
+
+template <int BM, int BN, int NMAT, bool OUT_F32>
+int launch_reduce(const GemmArgs& ga, hipStream_t st) {
+  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
+  const dim3 grid(static_cast<unsigned>((slots + kThreads - 1) / kThreads));
+  if (ga.splits == 2)
+    hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32, 2>), grid, dim3(kThreads), 0, st, ga);
+  else if (ga.splits == 4)
+    hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32, 4>), grid, dim3(kThreads), 0, st, ga);
+  else if (ga.splits == 8)
+    hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32, 8>), grid, dim3(kThreads), 0, st, ga);
+  else
+    hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32, 0>), grid, dim3(kThreads), 0, st, ga);
+  return check_launch("w8a16 gemm reduce kernel");
 }
 
 template <int BM, int BN, int NMAT, bool OUT_F32, int OCC, int LEAD>
@@ -878,10 +912,7 @@ int launch_cfg(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
                      dim3(kThreads), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
   if (rc || ga.splits == 1) return rc;
-  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
-  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
-                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
-  return check_launch("w8a16 gemm reduce kernel");
+  return launch_reduce<BM, BN, NMAT, OUT_F32>(ga, st);
 }
 
 template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int XLEAD, int OCC, int KG = 1>
@@ -892,10 +923,7 @@ int launch_k64(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
                      dim3(kThreads * KG), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
   if (rc || ga.splits == 1) return rc;
-  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
-  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
-                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
-  return check_launch("w8a16 gemm reduce kernel");
+  return launch_reduce<BM, BN, NMAT, OUT_F32>(ga, st);
 }
 
 template <int BM, int BN, int NMAT, bool OUT_F32, int WLEAD, int S, int OCC>
@@ -906,10 +934,7 @@ int launch_dma(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
                      dim3(kThreads), 0, st, x, ga);
   int rc = check_launch("w8a16 gemm kernel");
   if (rc || ga.splits == 1) return rc;
-  const int64_t slots = static_cast<int64_t>(ga.tiles) * BM * BN / 4;
-  hipLaunchKernelGGL((gemm_reduce_kernel<BM, BN, NMAT, OUT_F32>),
-                     dim3(static_cast<unsigned>((slots + kThreads - 1) / kThreads)), dim3(kThreads), 0, st, ga);
-  return check_launch("w8a16 gemm reduce kernel");
+  return launch_reduce<BM, BN, NMAT, OUT_F32>(ga, st);
 }
 
 // A short K over few tokens in one round trip (single matrices at 33..128

@@ -17,7 +17,7 @@ _SIG = "(const uint16_t *, const GemmArgs &, hipStream_t)"
 @pytest.mark.parametrize("plan, kernel, reduce", [
     (f"int pgs::(anonymous namespace)::launch_k64{_SIG} [BM = 64, BN = 128, NMAT = 1, OUT_F32 = false, WLEAD = 2, "
      "XLEAD = 2, OCC = 2, KG = 2] | grid=512 splits=4 | then gemm_reduce_kernel",
-     "gemm_k64_kernel<64, 128, 1, false, 2, 2, 2, 2>", "gemm_reduce_kernel<64, 128, 1, false>"),
+     "gemm_k64_kernel<64, 128, 1, false, 2, 2, 2, 2>", "gemm_reduce_kernel<64, 128, 1, false"),
     (f"int pgs::(anonymous namespace)::launch_dma{_SIG} [BM = 128, BN = 64, NMAT = 2, OUT_F32 = false, WLEAD = 2, "
      "S = 3, OCC = 3] | grid=688 splits=1",
      "gemm_dma_kernel<128, 64, 2, false, 2, 3, 3>", None),
