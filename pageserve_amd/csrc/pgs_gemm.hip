@@ -942,21 +942,26 @@ int launch_dma(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 // The stepped kernels spend ~1 us per 64-k step there waiting on their own
 // pipeline (every step's loads, LDS stores and barrier on the critical path
 // of few waves) while the work per step is tiny.  Here a workgroup of 16
-// waves owns 16 tokens x 16 NT weight rows: every wave issues all of its loads
-// at once -- a sixteenth of the 16 x K activation tile by LDS DMA (each
-// lane's 16 bytes placed at their swizzled home, rows past M read as zero)
-// and its weight blocks (one 16-row tile, every NG-th 64-k chunk, CPG
+// waves owns 16 TM tokens x 16 NT weight rows: every wave issues all of its
+// loads at once -- a sixteenth of the 16 TM x K activation tile by LDS DMA
+// (each lane's 16 bytes placed at their swizzled home, rows past M read as
+// zero) and its weight blocks (one 16-row tile, every NG-th 64-k chunk, CPG
 // blocks) into registers -- then one wait and one barrier, its MFMAs, and
 // the NG K groups summed through LDS in a fixed order.  NT = 4, 2 or 1
-// 16-row tiles per workgroup (NG = 16 / NT K groups).
-template <int CPG, int NT, bool OUT_F32>
+// 16-row tiles per workgroup (NG = 16 / NT K groups); TM = 1 or 2 16-token
+// tiles.  Once the data is in, the int8 -> bf16 widening (12 VALU per 8
+// weights) is what takes the time: with TM = 2 each widened operand feeds
+// two MFMAs (o_proj at 128 tokens: 2.5 us of the 16-token tile's 6.6 us
+// launch span are its MFMA phase, with every byte already landed).
+template <int CPG, int NT, bool OUT_F32, int TM = 1>
 __global__ __launch_bounds__(1024) void gemm_once_kernel(const uint16_t* __restrict__ x, GemmArgs ga) {
-  constexpr int BM = 16, BN = 16 * NT, NG = 16 / NT;
+  constexpr int BM = 16 * TM, BN = 16 * NT, NG = 16 / NT;
   constexpr int CH = NG * CPG;       // chunks (64 k) the activation tile holds
-  constexpr int CHUNK = BM * kBK;    // bf16 elements of one chunk block (2 KiB)
+  constexpr int CHUNK = BM * kBK;    // bf16 elements of one chunk block (2 TM KiB)
   constexpr int SLICES = CH * CHUNK * 2 / 1024;  // 1 KiB DMA slices of the tile
   constexpr int SPW = SLICES / 16;               // per wave
-  static_assert(SPW * 16 == SLICES && NT * NG == 16, "whole slices per wave; 16 waves");
+  static_assert(SPW * 16 == SLICES && NT * NG == 16 && (TM == 1 || TM == 2), "whole slices per wave; 16 waves");
+  static_assert(CH * CHUNK * 2 <= 128 * 1024, "the activation tile fits the LDS");
   __shared__ __attribute__((aligned(16))) uint16_t xs[CH * CHUNK];
   const GroupArgs& a = ga.g;
   const int M = ga.M, K = ga.K;
@@ -983,7 +988,7 @@ __global__ __launch_bounds__(1024) void gemm_once_kernel(const uint16_t* __restr
     const int sl = wave * SPW + j;
     if (sl < nslices) {
       const int p = sl * 64 + lane;
-      const int c = p >> 7, row = (p >> 3) & 15, pc = p & 7;
+      const int c = p / (BM * 8), row = (p >> 3) % BM, pc = p & 7;
       const int lc = pc ^ (row & 7) ^ ((row >> 3) & 1);
       dma16(xres, xs + sl * 512, row * K * 2 + c * 128 + lc * 16, 0);
     }
@@ -1013,42 +1018,53 @@ __global__ __launch_bounds__(1024) void gemm_once_kernel(const uint16_t* __restr
   __builtin_amdgcn_s_waitcnt(kWait);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  // token tile t's rows sit 16 t rows on, with the same swizzle
   const int bofs0 = swz(lr, 2 * lg), bofs1 = swz(lr, 2 * lg + 1);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int j = 0; j < CPG; ++j) {
     const int c = j * NG + grp;
     if (c < kb) {
       const uint16_t* blk = xs + c * CHUNK;
-      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(blk + bofs0);
-      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(blk + bofs1);
-      acc = mfma16x16x32(i8x8_to_bf16x8(w[j][0], w[j][1]), b0, acc);
-      acc = mfma16x16x32(i8x8_to_bf16x8(w[j][2], w[j][3]), b1, acc);
+      const bf16x8 a0 = i8x8_to_bf16x8(w[j][0], w[j][1]), a1 = i8x8_to_bf16x8(w[j][2], w[j][3]);
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(blk + t * 16 * kBK + bofs0);
+        const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(blk + t * 16 * kBK + bofs1);
+        acc[t] = mfma16x16x32(a0, b0, acc[t]);
+        acc[t] = mfma16x16x32(a1, b1, acc[t]);
+      }
     }
   }
   __builtin_amdgcn_s_setprio(0);
-  // the K quarters meet in LDS (the tile's space, free after this barrier)
+  // the K groups meet in LDS (the tile's space, free after this barrier)
   __syncthreads();
   f32x4* red = reinterpret_cast<f32x4*>(xs);
-  red[(grp * NT + nt) * 64 + lane] = acc;
+#pragma unroll
+  for (int t = 0; t < TM; ++t) red[((grp * NT + nt) * TM + t) * 64 + lane] = acc[t];
   __syncthreads();
   if (grp != 0) return;
-  f32x4 v = red[nt * 64 + lane];
-#pragma unroll
-  for (int q = 1; q < NG; ++q) v += red[(q * NT + nt) * 64 + lane];
-  const int m = m0 + lr;
-  if (m >= M) return;
   void* y = pick(a.y, g);
-  store_rows4<1, OUT_F32>(a, g, N, m, nb, e, v, v, y, vec_out<OUT_F32>(y, N));
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    f32x4 v = red[(nt * TM + t) * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < NG; ++q) v += red[((q * NT + nt) * TM + t) * 64 + lane];
+    const int m = m0 + 16 * t + lr;
+    if (m < M) store_rows4<1, OUT_F32>(a, g, N, m, nb, e, v, v, y, vec_out<OUT_F32>(y, N));
+  }
 }
 
-template <int CPG, int NT, bool OUT_F32>
+template <int CPG, int NT, bool OUT_F32, int TM = 1>
 int launch_once(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
   if (ga.splits != 1 || ga.K % kBK != 0 || ga.K > 16 / NT * CPG * kBK)
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 gemm: one-shot tile for K=%d", ga.K);
   note_launch(__PRETTY_FUNCTION__, ga.tiles, 1);
-  hipLaunchKernelGGL((gemm_once_kernel<CPG, NT, OUT_F32>), dim3(static_cast<unsigned>(ga.tiles)), dim3(1024), 0, st, x, ga);
+  hipLaunchKernelGGL((gemm_once_kernel<CPG, NT, OUT_F32, TM>), dim3(static_cast<unsigned>(ga.tiles)), dim3(1024), 0, st,
+                     x, ga);
   return check_launch("w8a16 gemm kernel");
 }
 
@@ -1081,8 +1097,14 @@ int launch_bm(const uint16_t* x, const GemmArgs& ga, hipStream_t st) {
 template <int NMAT, bool OUT_F32>
 int launch_plan(const uint16_t* x, const GemmArgs& ga, const GemmPlan& plan, hipStream_t st) {
   if constexpr (NMAT == 1) {
-    // one-shot 16-token tiles (K <= 2048): 64, 32 or 16 rows in 4, 8 or 16 K groups
-    if (plan.bm == 16) {
+    // one-shot 16- or 32-token tiles (K <= 2048): 64, 32 or 16 rows in 4, 8
+    // or 16 K groups
+    if (plan.once) {
+      if (plan.bm == 32) {
+        if (plan.bn == 64) return launch_once<8, 4, OUT_F32, 2>(x, ga, st);
+        if (plan.bn == 32) return launch_once<4, 2, OUT_F32, 2>(x, ga, st);
+        return launch_once<2, 1, OUT_F32, 2>(x, ga, st);
+      }
       if (plan.bn == 64) return launch_once<8, 4, OUT_F32>(x, ga, st);
       if (plan.bn == 32) return launch_once<4, 2, OUT_F32>(x, ga, st);
       return launch_once<2, 1, OUT_F32>(x, ga, st);
@@ -1146,25 +1168,45 @@ GemmPlan plan_gemm(int m, int k, int nmat, const int32_t* n, int members, bool c
     for (int i = 0; i < members; ++i) tiles_n += (n[i] + p.bn - 1) / p.bn;
   }
   if (mid) {
-    // a single matrix with K <= 2048: one-shot 16-token tiles of 16, 32 or 64
-    // rows, the smallest whose count fills the 256 CUs at most once (o_proj
-    // at 64 tokens 6.1 vs 9.3 us, q|k|v at 96 tokens 7.8 vs 9.2 us); more
-    // tiles than that run past one round and lose to the stepped kernel
-    // (q|k|v at 128 tokens 11.0 vs 9.2 us)
+    // a single matrix with K <= 2048: one-shot tiles of 16 or 32 tokens and
+    // 16, 32 or 64 rows, the fewest rows whose count fills the 256 CUs at
+    // most once (o_proj at 64 tokens 6.1 vs 9.3 us, q|k|v at 96 tokens 7.8 vs
+    // 9.2 us); more tiles than that run past one round and lose to the
+    // stepped kernel (q|k|v at 128 tokens 11.0 vs 9.2 us).  Of the two token
+    // heights the one with more tiles, and at equal counts 32 tokens (each
+    // widened weight feeds two MFMAs: o_proj at 96 / 128 tokens 7.0 / 7.1 vs
+    // 7.4 / 7.7 us); 16 tokens up to 64 (6.0 vs 6.9 us for o_proj at 64,
+    // where 32 would halve the tiles)
     if (nmat == 1 && kb <= 32) {
-      for (int nt = 1; nt <= 4; nt *= 2) {
-        int tn = 0;
-        for (int i = 0; i < members; ++i) tn += (n[i] + 16 * nt - 1) / (16 * nt);
-        if (static_cast<int64_t>((m + 15) / 16) * tn <= 256) {
-          p.bm = 16;
-          p.bn = 16 * nt;
-          p.kg = 16 / nt;
-          p.tiles_m = (m + 15) / 16;
-          p.tiles_n = tn;
-          p.tiles = p.tiles_m * tn;
-          p.splits = 1;
-          return p;
+      int best_bm = 0, best_nt = 0, best_tn = 0;
+      int64_t best_tiles = 0;
+      for (int bm = 16; bm <= 32; bm *= 2) {
+        if (bm == 32 && m <= 64) continue;
+        for (int nt = 1; nt <= 4; nt *= 2) {
+          int tn = 0;
+          for (int i = 0; i < members; ++i) tn += (n[i] + 16 * nt - 1) / (16 * nt);
+          const int64_t tiles = static_cast<int64_t>((m + bm - 1) / bm) * tn;
+          if (tiles <= 256) {
+            if (tiles > best_tiles || (tiles == best_tiles && bm == 32)) {
+              best_bm = bm;
+              best_nt = nt;
+              best_tn = tn;
+              best_tiles = tiles;
+            }
+            break;
+          }
         }
+      }
+      if (best_tiles > 0) {
+        p.once = true;
+        p.bm = best_bm;
+        p.bn = 16 * best_nt;
+        p.kg = 16 / best_nt;
+        p.tiles_m = (m + best_bm - 1) / best_bm;
+        p.tiles_n = best_tn;
+        p.tiles = static_cast<int>(best_tiles);
+        p.splits = 1;
+        return p;
       }
     }
     p.bm = (nmat == 1 && kb <= 64) ? 32 : 64;

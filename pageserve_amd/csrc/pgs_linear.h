@@ -67,6 +67,7 @@ struct GemmPlan {
   int kg;         // K groups of four waves per workgroup (K % 64 == 0 kernel)
   int tiles_m, tiles_n, tiles;
   int splits;     // workgroups per output tile along K
+  bool once;      // the one-shot tile (16 or 32 tokens, K <= 2048)
 };
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split);

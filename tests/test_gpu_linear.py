@@ -473,3 +473,37 @@ def test_narrow_tile_plan(gpu):
     qw, q, s, x, _ = _problem(gpu, 7768, 1024, 2048, 2048)
     qw.linear(bf16_gpu(x, gpu))
     assert narrow not in _plan_kernel() and "BN = 128" in _plan_kernel(), _plan_kernel()
+
+
+def test_one_shot_32_token_plan(gpu):
+    """65..128 tokens, one matrix, K <= 2048: one-shot tiles of 32 tokens
+    (launch_once<*, *, *, 2>, each widened weight fragment feeding two MFMAs)
+    where they give at least as many workgroups as 16-token tiles: o_proj's
+    shape at 96 and 128 tokens, a ragged M (97: one token in the last tile)
+    and N with a bias, and q|k|v at 128 tokens (64-row tiles) against the
+    full oracle; at 64 tokens and where 16-token tiles are more (100 x 300)
+    the 16-token tile stays."""
+    tm2 = "TM = 2"
+    for m, n, k, seed, want in ((96, 2048, 2048, 7781, "NT = 2"), (128, 2048, 2048, 7782, "NT = 2"),
+                                (97, 2048, 2048, 7783, "NT = 2"), (70, 1000, 1024, 7784, "NT = 1"),
+                                (64, 2048, 2048, 7785, None), (100, 300, 2048, 7786, None)):
+        qw, q, s, x, b = _problem(gpu, seed, m, n, k, bias=n != 2048)
+        y = to_np(qw.linear(bf16_gpu(x, gpu), bf16_gpu(b, gpu) if b is not None else None))
+        plan = _plan_kernel()
+        assert "launch_once" in plan, plan
+        assert (tm2 in plan) == (want is not None) and (want is None or want in plan), plan
+        report(y, O.linear(x, q, s, b), k, f"once m={m} n={n} k={k}", acc=O.acc_bound(x, q, s, b))
+    m, k = 128, 2048
+    x = activations(7787, m, k)
+    ws, qs, ss = [], [], []
+    for j, n in enumerate((2048, 256, 256)):
+        w = weights(7788 + j, n, k)
+        ws.append(Q.QuantizedWeight(torch.from_numpy(w).to(gpu)))
+        q, s = O.quantize_per_channel(w)
+        qs.append(q)
+        ss.append(s)
+    outs = Q.linear_group(bf16_gpu(x, gpu), ws)
+    plan = _plan_kernel()
+    assert "launch_once" in plan and tm2 in plan and "NT = 4" in plan, plan
+    for j in range(3):
+        report(to_np(outs[j]), O.linear(x, qs[j], ss[j]), k, f"once qkv[{j}]", acc=O.acc_bound(x, qs[j], ss[j]))
