@@ -19,8 +19,9 @@
 //
 // Roles inside a workgroup of 16 waves:
 //  * 15 streaming waves own a fixed list of 1 KiB weight loads (packed tile
-//    layout, folded 8-row units: two 64-k chunks per MFMA, as the skinny
-//    kernel's folded halves) over the four stages.  A wave keeps span_ring
+//    layout: whole 16-row blocks for gate|up; folded 8-row units elsewhere,
+//    two 64-k chunks per MFMA as the skinny kernel's folded halves) over
+//    the four stages.  A wave keeps span_ring
 //    loads in flight, issuing the next load as soon as one is consumed, so
 //    the next stage's weights arrive while the current dependency is being
 //    met.  Its waits are on its own loads and on workgroup barriers only:
@@ -116,18 +117,21 @@ using Qwen25_3B = Dims<2048, 11008, 2048, 256, 128>;
 // columns t + M j for the tokens' chunk j), as the skinny kernel's folded
 // halves; an item is one F*64-k slot of a unit (one 1 KiB load per matrix);
 // the items of a workgroup's units are dealt to the streaming waves in
-// contiguous runs of P.  F = 2 (8-row units) throughout: 4-row units
-// (F = 4) would balance gate|up better (10 or 11 units per workgroup instead
-// of 5 or 6) but read 64 of each 128 bytes of a cache line, the other half
-// belonging to another workgroup, often on another XCD: measured 31 against
-// 24.5 us per layer.
+// contiguous runs of P.  gate|up: F = 1, whole 16-row units (2 or 3 per
+// workgroup), so that every load is one contiguous packed block.  With
+// 8-row units (F = 2) a load reads half of two blocks whose other halves
+// another workgroup reads at another time, and the pair streams slower
+// (per step 888 against 910 us; 4-row units, F = 4, reading half lines:
+// 31 against 24.5 us per layer).  o_proj, down_proj and q|k|v: F = 2,
+// 8-row units, since their 128 (o, down) block rows would leave half the
+// CUs idle as whole units (and q|k|v pairs rows for RoPE).
 template <class DM, int M>
 struct Geo {
   static constexpr int H = DM::H, I = DM::I;
   // q and k heads in unit pairs (rows i and i + HD/2 of a head, for RoPE), v
   // units alone
   static constexpr int kQP = DM::NQ / 16, kKP = DM::NKV / 16, kVS = DM::NKV / 8;
-  static constexpr int fold(int) { return 2; }
+  static constexpr int fold(int s) { return s == 1 ? 1 : 2; }
   static constexpr int rows(int s) { return 16 / fold(s); }
   static constexpr int units(int s) { return s == 1 ? I / rows(1) : s == 3 ? (DM::NQ + 2 * DM::NKV) / 8 : H / 8; }
   static constexpr int U(int s) { return s == 3 ? 2 : cdiv(units(s), kSpanG); }
@@ -145,7 +149,7 @@ struct Geo {
   // B operand rows in LDS: [M][K + 64] bf16 (the pad staggers the tokens)
   static constexpr int ks(int s) { return kdim(s) + 64; }
   static constexpr int kBBytes = M * (cmax(H, I) + 64) * 2;
-  static constexpr int kPartFloats = kSpanSW * 2 * 2 * 8 * M;
+  static constexpr int kPartFloats = kSpanSW * 2 * 2 * 16 * M;  // room for 16-row units
   static constexpr int kOffB = 0;
   static constexpr int kOffLn = kOffB + kBBytes;  // two norm weights [H] bf16
   static constexpr int kOffPart = kOffLn + 2 * H * 2;
@@ -490,9 +494,10 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     });
     // partial tiles: output (token t, row r) of a folded unit is
     // sum_s C[r + R s][t + M s] (s < F, in order); C[i][j] sits in lane
-    // 16 (i / 4) + j, register i % 4.  F = 2: lanes t and 16 + t hold rows
-    // 0-3 and 4-7, partners 32 + M lanes on; F = 4: lane t holds rows 0-3,
-    // partners 16 + M, 2 (16 + M), 3 (16 + M) lanes on.
+    // 16 (i / 4) + j, register i % 4.  F = 1: lanes t, 16 + t, 32 + t and
+    // 48 + t hold rows 0-3 .. 12-15, no partners; F = 2: lanes t and 16 + t
+    // hold rows 0-3 and 4-7, partners 32 + M lanes on; F = 4: lane t holds
+    // rows 0-3, partners 16 + M, 2 (16 + M), 3 (16 + M) lanes on.
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
         }
         const int t = lane & 15;
         if (lane < 16 * (R / 4) && t < M) {
-          float* dst = part + ((wave * 2 + a) * 2 + mat) * (8 * M) + t * 8 + (lane >> 4) * 4;
+          float* dst = part + ((wave * 2 + a) * 2 + mat) * (16 * M) + t * R + (lane >> 4) * 4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) dst[i] = v[i];
         }
@@ -538,7 +543,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     float v = 0.f;
     for (int s = s_lo; s <= s_hi; ++s) {
       const int a = lu - (P * s) / IPU;
-      v += part[((s * 2 + a) * 2 + mat) * (8 * M) + t * 8 + r];
+      v += part[((s * 2 + a) * 2 + mat) * (16 * M) + t * G::rows(S) + r];
     }
     return v;
   };
