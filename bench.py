@@ -384,6 +384,7 @@ def span_timeline(dev, layers_n, m, command):
     polls = [[int(v) for v in t[:, 13 + g]] for g in range(3) for t in launches]
     poll_med = [statistics.median([statistics.median(p) for p in polls[g * layers_n:(g + 1) * layers_n]])
                 for g in range(3)]
+    poll_max = [max(max(p) for p in polls[g * layers_n:(g + 1) * layers_n]) for g in range(3)]
     lines = [f"# Decode span stage timeline, M={m}, Qwen2.5-3B ({layers_n} layers, one persistent launch per layer)",
              "", "Command (repository root):", "", "```", command, "```", "",
              "Per-workgroup timestamps (`s_memrealtime`, 100 MHz) written by lane 0 of each workgroup's control wave "
@@ -397,8 +398,9 @@ def span_timeline(dev, layers_n, m, command):
              f"min {min(spans):.2f}, max {max(spans):.2f}",
              f"- spread of the 256 workgroup starts: median {statistics.median(starts):.2f} us",
              f"- gap from a launch's last end to the next one's first start: median {statistics.median(gaps):.2f} us",
-             f"- polls per workgroup before each gather saw every word (median): x1 {poll_med[0]:.0f}, act "
-             f"{poll_med[1]:.0f}, x2 {poll_med[2]:.0f}", "",
+             f"- polls of wave 0 of each workgroup before each gather saw every word (median / max): x1 "
+             f"{poll_med[0]:.0f} / {poll_max[0]}, act {poll_med[1]:.0f} / {poll_max[1]}, x2 {poll_med[2]:.0f} / "
+             f"{poll_max[2]}", "",
              "| stage boundary | phase us (p50 over workgroups) | at us, p50 workgroup | at us, last workgroup |",
              "|---|---:|---:|---:|"]
     for name, d, a, b in rows:

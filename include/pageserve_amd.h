@@ -420,7 +420,7 @@ int pgs_w8a16_decode_span_test_hooks(int spin_limit, int force_giveup);
  * end of gate|up's stream, activations published, activations gathered,
  * end of down_proj's stream, x2 published, x2 gathered (next RMSNorm done),
  * end of q|k|v's stream, end of the launch; 13..15: polls of the three
- * gathers.  NULL turns it off.  Process-wide; the buffer must outlive the
+ * gathers (wave 0's).  NULL turns it off.  Process-wide; the buffer must outlive the
  * launches that write it, including every replay of a graph captured while
  * it was set (the launch holds its address).
  */

@@ -64,7 +64,9 @@
 // writes s_memrealtime (a constant 100 MHz clock) at every stage boundary
 // into slot (launch tag % slots) of the buffer, laid out [slots][256
 // workgroups][16] u64: entries 0..12 the marks below, 13..15 the poll
-// counts of the three gathers.  Without one, a mark is a uniform branch.
+// counts of the three gathers, as wave 0 saw them (it holds exchange
+// pieces at every token count; the control wave holds none at one token).
+// Without one, a mark is a uniform branch.
 #define PGS_SPAN_MARK(i)                                                    \
   do {                                                                      \
     if (tracing && tid == kSpanSW * 64) trow[i] = __builtin_amdgcn_s_memrealtime(); \
@@ -72,6 +74,10 @@
 #define PGS_SPAN_NOTE(i, v)                                   \
   do {                                                        \
     if (tracing && tid == kSpanSW * 64) trow[i] = (v);        \
+  } while (0)
+#define PGS_SPAN_POLLS(i, v)                                  \
+  do {                                                        \
+    if (tracing && tid == 0) trow[i] = (v);                   \
   } while (0)
 
 namespace pgs {
@@ -686,7 +692,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   }
   // every workgroup has read the epoch (it published with its tag)
   if (wg == 0 && tid == 0) st_agent(ws, ltag);
-  PGS_SPAN_NOTE(13, polls);
+  PGS_SPAN_POLLS(13, polls);
   barrier_lds();
   PGS_SPAN_MARK(4);
 
@@ -719,7 +725,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     give_up();
     return;
   }
-  PGS_SPAN_NOTE(14, polls);
+  PGS_SPAN_POLLS(14, polls);
   barrier_lds();
   PGS_SPAN_MARK(7);
 
@@ -750,7 +756,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     give_up();
     return;
   }
-  PGS_SPAN_NOTE(15, polls);
+  PGS_SPAN_POLLS(15, polls);
   barrier_lds();
   PGS_SPAN_MARK(10);
 

@@ -89,7 +89,8 @@ def decode_span_trace(buffer: torch.Tensor | None) -> None:
     contiguous int64 CUDA tensor of ``slots * 256 * 16`` entries) or off
     (None).  While on, each launch writes per-workgroup timestamps (100 MHz
     ticks) into ``buffer.view(slots, 256, 16)[tag % slots]``: entries 0..12
-    the :data:`TRACE_MARKS`, 13..15 the poll counts of the three gathers.
+    the :data:`TRACE_MARKS`, 13..15 the poll counts of the three gathers
+    (those of each workgroup's first wave).
     The buffer is kept referenced until tracing is turned off.  A HIP graph
     captured while tracing is on holds the buffer's address and writes to it
     on every replay: keep the buffer for as long as such a graph exists."""
