@@ -626,12 +626,14 @@ def prefill_workload(dev, layers_n, m, plan_path):
 def kernel_pattern(plan: str) -> tuple[str, str | None]:
     """The demangled kernel name (template argument list) of a launch plan
     string, and of its follow-up reduce kernel, if any."""
-    m = re.search(r"(launch_k64|launch_dma|launch_once|launch_cfg|launch_instance)\(.*?\) \[(.*?)\]", plan)
+    m = re.search(r"(launch_k64|launch_dma|launch_once|launch_cfg|launch_instance|launch_pair_tiles)\(.*?\) "
+                  r"\[(.*?)\]", plan)
     if not m:
         raise ValueError(f"unrecognised launch plan {plan!r}")
     vals = [kv.split(" = ")[1] for kv in m.group(2).split(", ")]
     name = {"launch_k64": "gemm_k64_kernel", "launch_dma": "gemm_dma_kernel", "launch_once": "gemm_once_kernel",
-            "launch_cfg": "gemm_kernel", "launch_instance": "skinny_kernel"}[m.group(1)]
+            "launch_cfg": "gemm_kernel", "launch_instance": "skinny_kernel",
+            "launch_pair_tiles": "pair_tiles_kernel"}[m.group(1)]
     reduce = None
     if "then gemm_reduce_kernel" in plan:
         reduce = "gemm_reduce_kernel<" + ", ".join(vals[:4])  # then the split count

@@ -656,6 +656,121 @@ int launch_shape(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
   }
 }
 
+// The SwiGLU pair at 14..16 tokens with a short K (K % 64 == 0, at most
+// NW * CPW chunks): RT row tiles per workgroup instead of one.  With one
+// tile per workgroup every workgroup loads the tokens' whole activation
+// rows for its 16 rows, as many bytes as its weights, and at 16 tokens each
+// of those loads touches 16 rows; here each activation fragment feeds the
+// RT tiles' gate and up MFMAs, and RT = 3 gives ceil(688 / 3) = 230
+// workgroups for an 11008-row pair, at most one per CU and at most 48 rows
+// per CU as before.  Wave w takes chunks w * CPW .. w * CPW + CPW - 1 of
+// every tile and issues all of its loads at once (one memory round trip);
+// the waves' partial tiles are summed through LDS in wave order (a fixed
+// order: reproducible), then each output thread applies silu(g s_g)(u s_u)
+// (engine/model.py:188-189).  Measured on the 11008 x 2048 pair (graphs over
+// 36 layers, us, one-tile plan -> this kernel): 16 tokens 11.56 -> 11.20,
+// 15: 11.36 -> 11.24, 14: 11.15 -> 11.02, but 13: 11.0 -> 11.1, 12: 10.8 ->
+// 10.9 and 9: 10.1 -> 10.5, hence 14..16 tokens; 8 waves x 4 chunks (11.9),
+// four tiles per workgroup (11.9) and two (13.0) are slower at 16 tokens.
+template <int RT, int NW, int CPW>
+__global__ __launch_bounds__(64 * NW, 1) void pair_tiles_kernel(const uint16_t* __restrict__ x, GroupArgs a, int M,
+                                                                int K, int tiles) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 15, kgrp = lane >> 4;
+  const int N = a.n[0];
+  const int nchunks = K >> 6;
+  const int t0 = blockIdx.x * RT;
+  // one buffer resource per tile and matrix over the tile's whole block
+  // row; a tile past the last reads zeros without touching memory
+  __amdgpu_buffer_rsrc_t wres[RT][2];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int mat = 0; mat < 2; ++mat) {
+      const bool ok = t0 + r < tiles;
+      wres[r][mat] = make_rsrc(a.q[mat] + (ok ? static_cast<int64_t>(t0 + r) * nchunks * 1024 : 0),
+                               ok ? static_cast<int64_t>(nchunks) * 1024 : 0);
+    }
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<int64_t>(M) * K * 2);
+  // B operand column lrow: token min(lrow, M - 1); this lane's 16 k of the chunk
+  const int xoff = min(lrow, M - 1) * K * 2 + kgrp * 32;
+
+  // output of this thread: tile er, token mm, tile row oi; its scales are
+  // requested first, from a clamped (valid) row, so no branch waits for them
+  const int idx = threadIdx.x;
+  const int er = min(idx >> 8, RT - 1), mm = (idx >> 4) & 15, oi = idx & 15;
+  const int row = (t0 + er) * 16 + oi;
+  const bool has_out = idx < 256 * RT && mm < M && row < N;
+  const int crow = min(row, N - 1);
+  const float sg = a.scale[0][crow], su = a.scale[1][crow];
+
+  u32x4 w[CPW][RT][2], xb[CPW][2];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int c = wave * CPW + j;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int mat = 0; mat < 2; ++mat)
+        w[j][r][mat] = __builtin_amdgcn_raw_buffer_load_b128(wres[r][mat], lane * 16, c * 1024, kLoadNT);
+    xb[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff, c * 128, 0);
+    xb[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xres, xoff + 16, c * 128, 0);
+  }
+  f32x4 acc[RT][2];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    // a chunk past K reads zero weights; its activations (the next token's
+    // row, or zeros) are masked too, so non-finite values cannot leak in
+    const uint32_t mask = wave * CPW + j < nchunks ? 0xffffffffu : 0u;
+    const bf16x8 b0 = __builtin_bit_cast(bf16x8, xb[j][0] & mask);
+    const bf16x8 b1 = __builtin_bit_cast(bf16x8, xb[j][1] & mask);
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int mat = 0; mat < 2; ++mat) {
+        acc[r][mat] = mfma16x16x32(i8x8_to_bf16x8(w[j][r][mat][0], w[j][r][mat][1]), b0, acc[r][mat]);
+        acc[r][mat] = mfma16x16x32(i8x8_to_bf16x8(w[j][r][mat][2], w[j][r][mat][3]), b1, acc[r][mat]);
+      }
+  }
+  __shared__ f32x4 part[NW][RT][2][64];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int mat = 0; mat < 2; ++mat) part[wave][r][mat][lane] = acc[r][mat];
+  __syncthreads();
+  if (has_out) {
+    // output (row oi, token mm) of a 16x16 tile: lane acc_lane(oi, mm), register oi % 4
+    const int ln = acc_lane(oi, mm), rg = oi & 3;
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) {
+      g += part[wv][er][0][ln][rg];
+      u += part[wv][er][1][ln][rg];
+    }
+    store_out<false>(a.y[0], static_cast<int64_t>(mm) * N + row, silu_f32(g * sg) * (u * su));
+  }
+}
+
+constexpr int kPairRT = 3, kPairNW = 16, kPairCPW = 2;
+
+// whether pair_tiles_kernel takes a SwiGLU pair launch
+bool pair_tiles_fits(const Problem& p, const SkinnyPlan& plan) {
+  return p.nmat == 2 && !p.out_f32 && !p.norm_w && plan.tm == 1 && plan.splits == 1 && p.m >= 14 && p.m <= 16 &&
+         p.k % 64 == 0 && p.k / 64 <= kPairNW * kPairCPW;
+}
+
+template <int RT, int NW, int CPW>
+int launch_pair_tiles(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
+  const int64_t grid = (static_cast<int64_t>(plan.tiles) + RT - 1) / RT;
+  note_launch(__PRETTY_FUNCTION__, grid, 1, nullptr);
+  hipLaunchKernelGGL((pair_tiles_kernel<RT, NW, CPW>), dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, st,
+                     p.x, p.args, p.m, p.k, plan.tiles);
+  return check_launch("w8a16 pair tiles kernel");
+}
+
 }  // namespace
 
 SkinnyPlan plan_skinny(int m, int k, int nmat, int tiles, bool can_split) {
@@ -733,6 +848,7 @@ int launch_skinny(Problem& p, const SkinnyPlan& plan, hipStream_t st) {
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: paired split without pair slots");
   if (plan.splits > 1 && !plan.pair && (!p.partials || p.partial_bytes < skinny_partial_bytes(plan, p.nmat)))
     return fail(PGS_ERR_INVALID_ARGUMENT, "w8a16 skinny: split-K plan without a large enough workspace");
+  if (pair_tiles_fits(p, plan)) return launch_pair_tiles<kPairRT, kPairNW, kPairCPW>(p, plan, st);
   if (p.nmat == 2) return launch_shape<2, false>(p, plan, st);
   return p.out_f32 ? launch_shape<1, true>(p, plan, st) : launch_shape<1, false>(p, plan, st);
 }

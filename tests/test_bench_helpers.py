@@ -29,6 +29,9 @@ _SIG = "(const uint16_t *, const GemmArgs &, hipStream_t)"
     ("int pgs::(anonymous namespace)::launch_instance(Problem &, const SkinnyPlan &, hipStream_t) [NW = 8, U = 2, "
      "NB = 2, NMAT = 2, OUT_F32 = false, K64 = true, FOLD = false, XM = 0, NORM = false, TM = 1] | grid=688 splits=1",
      "skinny_kernel<8, 2, 2, 2, false, true, false, 0, false, 1>", None),
+    ("int pgs::(anonymous namespace)::launch_pair_tiles(Problem &, const SkinnyPlan &, hipStream_t) [RT = 3, "
+     "NW = 16, CPW = 2] | grid=230 splits=1",
+     "pair_tiles_kernel<3, 16, 2>", None),
 ])
 def test_kernel_pattern_names_the_launched_instance(plan, kernel, reduce):
     assert bench.kernel_pattern(plan) == (kernel, reduce)

@@ -39,7 +39,12 @@ def _mlp_weights(gpu, seed, inter, hidden):
                                             # half full: 64-token tiles
                                             (160, 11008, 2048), (320, 1000, 2112),
                                             # two token blocks: unsplit, and a long K split into partials
-                                            (32, 11008, 2048), (24, 1000, 8192), (21, 300, 1040)])
+                                            (32, 11008, 2048), (24, 1000, 8192), (21, 300, 1040),
+                                            # 14..16 tokens, K <= 2048: three row tiles per workgroup
+                                            # (ragged N, tile counts not a multiple of three, a K of
+                                            # 17 chunks, a single chunk)
+                                            (14, 11008, 2048), (15, 1000, 2048), (16, 130, 1088),
+                                            (14, 48, 64), (16, 100, 2048)])
 def test_swiglu_matches_oracle(gpu, m, inter, hidden):
     ws = _mlp_weights(gpu, 10 + m + inter, inter, hidden)
     x = activations(m, m, hidden)
@@ -72,3 +77,21 @@ def test_swiglu_equals_unfused_composition(gpu):
     got = Q.swiglu(x, ws["gate"][0], ws["up"][0]).float()
     # same fp32 accumulations; silu rounding may differ by one bf16 ulp
     assert ((got - expect).abs() <= expect.abs() * 2 ** -7 + 1e-6).all()
+
+
+def test_pair_tiles_plan(gpu):
+    """14..16 tokens with K % 64 == 0 and at most 32 chunks run the pair as three
+    16-row tiles per workgroup (pair_tiles_kernel); 13 tokens and a 33-chunk K keep
+    the one-tile skinny plan.  Every case against the oracle."""
+    from pageserve_amd import _native
+
+    for m, inter, hidden, want in ((16, 11008, 2048, True), (14, 1000, 2048, True), (15, 35, 128, True),
+                                   (13, 11008, 2048, False), (16, 1000, 2112, False)):
+        ws = _mlp_weights(gpu, 900 + m + inter, inter, hidden)
+        x = activations(950 + m, m, hidden)
+        act = Q.swiglu(bf16_gpu(x, gpu), ws["gate"][0], ws["up"][0])
+        plan = _native.last_plan()
+        assert ("launch_pair_tiles" in plan) == want, plan
+        ref = O.swiglu(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2])
+        acc = O.swiglu_acc(x, ws["gate"][1], ws["gate"][2], ws["up"][1], ws["up"][2])
+        report(to_np(act), ref, hidden, f"pair tiles m={m} n={inter} k={hidden}", acc=acc)
