@@ -1069,7 +1069,7 @@ def main():
                     help="write the single-launch decode chain's stage timeline (markdown) to OUT and exit")
     ap.add_argument("--prefill-workload", type=int, metavar="M",
                     help="run only the prefill sweep's launches once per layer at M tokens (counter passes)")
-    ap.add_argument("--plan-file", default="gpurun_out/prefill_plans.json",
+    ap.add_argument("--plan-file", default="prefill_plans.json",
                     help="where --prefill-workload records each launch kind's kernel instance")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "PLAN_FILE"),
                     help="reduce a rocprofv3 --pmc pass over --prefill-workload to an MFMA table (no GPU)")
