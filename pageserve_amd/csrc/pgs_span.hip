@@ -91,6 +91,15 @@ constexpr int kSpanThreads = 64 * (kSpanSW + 1);  // + one control wave
 // the control wave polls an exchange delays the poll; the ring only has to
 // cover the memory latency at the CU's share of the bandwidth.
 constexpr int kSpanRingDefault = 4;
+// The normalising gathers (x1, x2: 8 KiB per workgroup at one token) issue
+// a second poll this many s_sleep units (64 clocks each) after the first
+// without waiting for it: the first, issued right behind the workgroup's
+// own publish, usually misses the slowest publishers' words, and the early
+// second poll saves part of a round trip (per step 882 against 892 us).  The
+// activation gather (44 KiB per workgroup) polls one at a time: reading it
+// twice slows the down_proj stream behind it (with early second polls in all
+// three gathers: 932-955 against 891 us).
+constexpr int kEarlyPoll = 16;
 constexpr int kSlot = 128;                        // exchange bytes per 8-row unit (8 rows x <= 4 tokens x 4 B)
 constexpr int kHeader = 256;                      // workspace header: [0] epoch, [1] error word
 constexpr int kSC1 = 16;                          // cache policy: sc1 (agent scope)
@@ -315,8 +324,9 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
   auto fresh = [&](const u32x4& x) {
     return (x[0] >> 16) == want && (x[1] >> 16) == want && (x[2] >> 16) == want && (x[3] >> 16) == want;
   };
-  // Each wave polls until its own pieces are fresh, and only then issues
-  // (on_poll) the next stage's first loads: a wave's loads return in
+  // Each wave polls until its own pieces are fresh (NORM: the first two
+  // polls kEarlyPoll apart, without waiting between them), and only then
+  // issues (on_poll) the next stage's first loads: a wave's loads return in
   // order, so a poll issued behind its own weight loads would wait for
   // them.  Then the workgroup-wide check (which also makes a give-up
   // uniform).
@@ -325,16 +335,41 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
 #pragma unroll
   for (int i = 0; i < NPT; ++i)
     if (tid + kSpanThreads * i < NP) stale |= 1u << i;
-  for (int spin = 0;; ++spin) {
+  int spin = 0;
+  if constexpr (NORM && kEarlyPoll > 0) {
+    u32x4 w[NPT];
 #pragma unroll
     for (int i = 0; i < NPT; ++i)
       if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
+    __builtin_amdgcn_s_sleep(kEarlyPoll);
 #pragma unroll
     for (int i = 0; i < NPT; ++i)
-      if ((stale & (1u << i)) && fresh(v[i])) stale &= ~(1u << i);
-    polls = spin + 1;
-    if (!__any(stale != 0) || spin >= spin_limit) break;
-    __builtin_amdgcn_s_sleep(1);
+      if (stale & (1u << i)) w[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      if (!(stale & (1u << i))) continue;
+      if (fresh(v[i])) {
+        stale &= ~(1u << i);
+      } else if (fresh(w[i])) {
+        v[i] = w[i];
+        stale &= ~(1u << i);
+      }
+    }
+    polls = 2;
+    spin = 2;
+  }
+  if (__any(stale != 0)) {
+    for (;; ++spin) {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i)
+        if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
+#pragma unroll
+      for (int i = 0; i < NPT; ++i)
+        if ((stale & (1u << i)) && fresh(v[i])) stale &= ~(1u << i);
+      polls = spin + 1;
+      if (!__any(stale != 0) || spin >= spin_limit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
   on_poll();
   if (block_any(stale != 0, any_words, seq)) return false;
