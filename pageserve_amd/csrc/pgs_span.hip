@@ -372,10 +372,11 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
     }
   }
   on_poll();
-  if (block_any(stale != 0, any_words, seq)) return false;
   // piece pc: unit pc / 2M (rows 8 unit ..), token (pc % 2M) / 2, rows
   // 8 unit + 4 (pc % 2) + e for its words e = 0..3
-  float r_t[M];
+  // NORM: each wave's sum of squares goes to LDS before the workgroup-wide
+  // check, whose barrier then serves both (a give-up discards it)
+  float* ssq = reinterpret_cast<float*>(smem + off_ssq);
   if constexpr (NORM) {
     float ss[M];
 #pragma unroll
@@ -392,7 +393,6 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
           if (pc < NP && t == tt) ss[tt] += x * x;
       }
     }
-    float* ssq = reinterpret_cast<float*>(smem + off_ssq);
 #pragma unroll
     for (int t = 0; t < M; ++t) {
       float x = ss[t];
@@ -400,7 +400,10 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
       for (int o = 1; o < 64; o <<= 1) x += __shfl_xor(x, o);
       if (lane == 0) ssq[wave * M + t] = x;
     }
-    barrier_lds();
+  }
+  if (block_any(stale != 0, any_words, seq)) return false;
+  float r_t[M];
+  if constexpr (NORM) {
 #pragma unroll
     for (int t = 0; t < M; ++t) {
       float tot = 0.f;
