@@ -576,7 +576,10 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   uint32_t tag = 0;
   float so_r = 0.f, sd_r = 0.f, res_r = 0.f, x1_r = 0.f;
   float sg_r[NG], su_r[NG];
-  float sq_r[2], bq_r[2], cs_r[4];
+  // q|k|v epilogue operands as loaded (raw bits: converted where used)
+  uint32_t sq_b[2] = {0u, 0u};
+  uint16_t bq_b[2] = {0, 0}, cs_b[4] = {0, 0, 0, 0};
+  bool bq_on[2] = {false, false};
   int qmem = 0, qrow[2] = {0, 0};
 
   // reduces unit lu's partial tiles of stage S for output (t, r), matrix mat
@@ -597,6 +600,42 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
       return true;
     }
     return false;
+  };
+
+  // The q|k|v epilogue operands (scales, bias, RoPE cos/sin), used only at
+  // the launch's end.  The control wave requests them once the x1 gather is
+  // done, when nothing of its own is in flight, and they have landed long
+  // before its next wait: loaded in the prologue they make the workgroups
+  // with q|k|v units publish x1 last.  The loads are unconditional -- an
+  // absent operand reads a valid stand-in address -- so that the number of
+  // loads in flight is the same on every path, and their raw bits stay in
+  // registers until the epilogue, so that nothing waits for them earlier.
+  auto load_qkv_operands = [&] {
+    const int t = cmin(lane / 8, M - 1), r = lane % 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int mem = 0, row0 = 0;
+      const URef u = unit_ref<DM, M, 3>(p, wg, j, 0, &mem, &row0);
+      qrow[j] = row0 + r;
+      if (j == 0) qmem = mem;
+      const bool ok = has_qkv && u.ok;
+      const uint16_t* b = ok ? pick_early(p.bqkv, mem) : nullptr;
+      const float* sptr = ok ? pick_early(p.sqkv, mem) + row0 + r : p.so + r;
+      const uint16_t* bptr = b ? b + row0 + r : p.resid + r;
+      sq_b[j] = __builtin_bit_cast(uint32_t, *sptr);
+      bq_b[j] = *bptr;
+      bq_on[j] = b != nullptr;
+    }
+    constexpr int HD = DM::HD;
+    const bool rope = has_qkv && p.cos && qmem < 2;
+    const int i = qrow[0] % HD;  // < HD / 2: the pair's first row
+    const int64_t base = static_cast<int64_t>(t) * HD;
+    const uint16_t* cp = rope ? p.cos + base + i : p.resid;
+    const uint16_t* sp = rope ? p.sin + base + i : p.resid;
+    cs_b[0] = cp[0];
+    cs_b[1] = sp[0];
+    cs_b[2] = cp[HD / 2];
+    cs_b[3] = sp[HD / 2];
   };
 
   const bool tracing = p.trace != nullptr;
@@ -640,33 +679,6 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
       sg_r[i] = p.sg[R1 * g + r];
       su_r[i] = p.su[R1 * g + r];
     }
-    if (has_qkv) {
-      const int t = cmin(lane / 8, M - 1), r = lane % 8;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        int mem = 0, row0 = 0;
-        const URef u = unit_ref<DM, M, 3>(p, wg, j, 0, &mem, &row0);
-        sq_r[j] = bq_r[j] = 0.f;
-        qrow[j] = row0 + r;
-        if (j == 0) qmem = mem;
-        if (u.ok) {
-          sq_r[j] = pick_early(p.sqkv, mem)[row0 + r];
-          const uint16_t* b = pick_early(p.bqkv, mem);
-          if (b) bq_r[j] = bf16_bits_to_f32(b[row0 + r]);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) cs_r[c] = 0.f;
-      if (p.cos && qmem < 2) {
-        constexpr int HD = DM::HD;
-        const int i = qrow[0] % HD;  // < HD / 2: the pair's first row
-        const int64_t base = static_cast<int64_t>(t) * HD;
-        cs_r[0] = bf16_bits_to_f32(p.cos[base + i]);
-        cs_r[1] = bf16_bits_to_f32(p.sin[base + i]);
-        cs_r[2] = bf16_bits_to_f32(p.cos[base + i + HD / 2]);
-        cs_r[3] = bf16_bits_to_f32(p.sin[base + i + HD / 2]);
-      }
-    }
   } else {
     zero_acc();
     prime(std::integral_constant<int, 0>{});
@@ -692,7 +704,13 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
         *reinterpret_cast<u32x4*>(smem + G::kOffLn + H * 2 + pc * 16) = lnn_v[i];
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+    // the epilogue operands have arrived: redefining them here (an empty
+    // asm) tells the compiler so, which keeps it from waiting for loads
+    // issued later wherever they are used
+    asm volatile("" : "+v"(so_r), "+v"(sd_r), "+v"(res_r));
+#pragma unroll
+    for (int i = 0; i < NG; ++i) asm volatile("" : "+v"(sg_r[i]), "+v"(su_r[i]));
   }
   barrier_lds();
   if (abort_now()) return;
@@ -728,6 +746,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     give_up();
     return;
   }
+  if (control) load_qkv_operands();
   // every workgroup has read the epoch (it published with its tag)
   if (wg == 0 && tid == 0) st_agent(ws, ltag);
   PGS_SPAN_POLLS(13, polls);
@@ -809,11 +828,25 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     if (u0.ok) {
       uint16_t* y = pick_early(p.yqkv, mem);
       const int n = mem == 0 ? DM::NQ : DM::NKV;
+      // (the empty asm makes the loaded bits opaque up to here: the compiler
+      // would otherwise convert them, and wait for the loads, where they
+      // were issued)
+      asm volatile("" : "+v"(sq_b[0]), "+v"(sq_b[1]), "+v"(bq_b[0]), "+v"(bq_b[1]), "+v"(cs_b[0]), "+v"(cs_b[1]),
+                   "+v"(cs_b[2]), "+v"(cs_b[3]));
+      float sq_r[2], bq_r[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        sq_r[j] = __builtin_bit_cast(float, sq_b[j]);
+        bq_r[j] = bq_on[j] ? bf16_bits_to_f32(bq_b[j]) : 0.f;
+      }
       const float y0 = bf16r(reduce(std::integral_constant<int, 3>{}, 0, 0, t, r) * sq_r[0] + bq_r[0]);
       if (mem < 2) {
         const float y1 = bf16r(reduce(std::integral_constant<int, 3>{}, 1, 0, t, r) * sq_r[1] + bq_r[1]);
         float o0 = y0, o1 = y1;
         if (p.cos) {
+          float cs_r[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) cs_r[c] = bf16_bits_to_f32(cs_b[c]);
           // engine/model.py:53-56 with rotate_half (:37-39), the reference's roundings
           o0 = bf16r(bf16r(y0 * cs_r[0]) + bf16r(-y1 * cs_r[1]));
           o1 = bf16r(bf16r(y1 * cs_r[2]) + bf16r(y0 * cs_r[3]));
