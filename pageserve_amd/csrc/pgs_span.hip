@@ -583,15 +583,25 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
   int qmem = 0, qrow[2] = {0, 0};
 
   // reduces unit lu's partial tiles of stage S for output (t, r), matrix mat
+  // (a unit's items span at most cdiv(IPU, P) + 1 waves: all of their
+  // partials are read before the first add, in a loop of that fixed length,
+  // since a bound that depends on the lane would serialise the LDS reads;
+  // the sum is the same, in wave order)
   auto reduce = [&](auto SI, int lu, int mat, int t, int r) {
     constexpr int S = decltype(SI)::value;
-    constexpr int P = G::P(S), IPU = G::ipu(S);
+    constexpr int P = G::P(S), IPU = G::ipu(S), KMAX = cdiv(IPU, P) + 1;
     const int s_lo = lu * IPU / P, s_hi = cmin(kSpanSW - 1, ((lu + 1) * IPU - 1) / P);
-    float v = 0.f;
-    for (int s = s_lo; s <= s_hi; ++s) {
-      const int a = lu - (P * s) / IPU;
-      v += part[((s * 2 + a) * 2 + mat) * (16 * M) + t * G::rows(S) + r];
+    float pv[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int s = cmin(s_lo + k, kSpanSW - 1);
+      const int a = cmin(cmax(lu - (P * s) / IPU, 0), 1);
+      pv[k] = part[((s * 2 + a) * 2 + mat) * (16 * M) + t * G::rows(S) + r];
     }
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+      if (s_lo + k <= s_hi) v += pv[k];
     return v;
   };
   auto abort_now = [&] {
