@@ -868,7 +868,6 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
       }
     }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   PGS_SPAN_MARK(12);
 }
 
