@@ -59,7 +59,9 @@ struct GemmArgs {
 };
 
 // Split-K partial tile in lane order: [tile][split][mat][nt][mt][lane] x f32x4
-// (the reduce kernel reads the same order).
+// (the reduce kernel reads the same order).  Written and read once each,
+// with the non-temporal policy (down_proj at 128 / 512 tokens 18.4 / 37.5
+// against 19.2 / 37.9 us with the default one).
 template <int TN, int TM, int NMAT, typename Args>
 __device__ __forceinline__ void store_partials(const f32x4 (&acc)[NMAT][TN][TM], const Args& ga, int t, int s, int wave,
                                                int lane) {
@@ -70,7 +72,8 @@ __device__ __forceinline__ void store_partials(const f32x4 (&acc)[NMAT][TN][TM],
 #pragma unroll
     for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
-      for (int mt = 0; mt < TM; ++mt) part[mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane] = acc[mat][nt][mt];
+      for (int mt = 0; mt < TM; ++mt)
+        __builtin_nontemporal_store(acc[mat][nt][mt], part + mat * SLOTS + ((wave * TN + nt) * TM + mt) * 64 + lane);
 }
 
 // Epilogue operands of four consecutive output rows nb .. nb+3 (clamped to
@@ -871,7 +874,7 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GemmArgs ga) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-      for (int sp = 0; sp < SPL; ++sp) pv[mat][sp] = part[(sp * NMAT + mat) * SLOTS + slot];
+      for (int sp = 0; sp < SPL; ++sp) pv[mat][sp] = __builtin_nontemporal_load(part + (sp * NMAT + mat) * SLOTS + slot);
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       v[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
