@@ -91,15 +91,18 @@ constexpr int kSpanThreads = 64 * (kSpanSW + 1);  // + one control wave
 // the control wave polls an exchange delays the poll; the ring only has to
 // cover the memory latency at the CU's share of the bandwidth.
 constexpr int kSpanRingDefault = 4;
-// The normalising gathers (x1, x2: 8 KiB per workgroup at one token) issue
-// a second poll this many s_sleep units (64 clocks each) after the first
-// without waiting for it: the first, issued right behind the workgroup's
-// own publish, usually misses the slowest publishers' words, and the early
-// second poll saves part of a round trip (per step 882 against 892 us).  The
-// activation gather (44 KiB per workgroup) polls one at a time: reading it
-// twice slows the down_proj stream behind it (with early second polls in all
-// three gathers: 932-955 against 891 us).
-constexpr int kEarlyPoll = 16;
+// The waves that hold pieces of a normalising gather (x1, x2: 8 KiB per
+// workgroup at one token) wait this many s_sleep units (64 clocks each)
+// after the workgroup's own publish before their first poll: issued at once
+// it misses the slowest publishers' words, and the second poll behind it
+// comes a round trip later.  One poll at about the time the last words
+// become visible needs no second in most workgroups, and reads the exchange
+// once (per step 822-824 against 846 us with two polls 16 units apart; 20 /
+// 24 / 32 units: 825 / 825 / 823 us).  The waves without pieces do not wait:
+// they issue the next stage's first loads at once.  The activation gather
+// (44 KiB per workgroup, pieces in every wave) polls at once (a delay of 16 /
+// 24 / 32 units: +1 / +5 / +10 us per step).
+constexpr int kNormPollDelay = 28;
 constexpr int kSlot = 128;                        // exchange bytes per 8-row unit (8 rows x <= 4 tokens x 4 B)
 constexpr int kHeader = 256;                      // workspace header: [0] epoch, [1] error word
 constexpr int kSC1 = 16;                          // cache policy: sc1 (agent scope)
@@ -309,7 +312,7 @@ __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to
 // the 16 waves in order); otherwise the values as they are.  The B operand
 // is [M][KS] bf16 in LDS.  Returns false (the same for every thread) after
 // spin_limit polls.
-template <int M, int K, int KS, bool NORM, class OnPoll>
+template <int M, int K, int KS, bool NORM, int DELAY, class OnPoll>
 __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* smem, int off_b, int off_ln,
                                          int off_ssq, int* any_words, int& seq, uint32_t want, int spin_limit,
                                          float eps, int& polls, OnPoll&& on_poll) {
@@ -324,8 +327,8 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
   auto fresh = [&](const u32x4& x) {
     return (x[0] >> 16) == want && (x[1] >> 16) == want && (x[2] >> 16) == want && (x[3] >> 16) == want;
   };
-  // Each wave polls until its own pieces are fresh (NORM: the first two
-  // polls kEarlyPoll apart, without waiting between them), and only then
+  // Each wave polls until its own pieces are fresh (a wave that holds
+  // pieces waits DELAY s_sleep units before its first poll), and only then
   // issues (on_poll) the next stage's first loads: a wave's loads return in
   // order, so a poll issued behind its own weight loads would wait for
   // them.  Then the workgroup-wide check (which also makes a give-up
@@ -335,31 +338,9 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
 #pragma unroll
   for (int i = 0; i < NPT; ++i)
     if (tid + kSpanThreads * i < NP) stale |= 1u << i;
-  int spin = 0;
-  if constexpr (NORM && kEarlyPoll > 0) {
-    u32x4 w[NPT];
-#pragma unroll
-    for (int i = 0; i < NPT; ++i)
-      if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
-    __builtin_amdgcn_s_sleep(kEarlyPoll);
-#pragma unroll
-    for (int i = 0; i < NPT; ++i)
-      if (stale & (1u << i)) w[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
-#pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-      if (!(stale & (1u << i))) continue;
-      if (fresh(v[i])) {
-        stale &= ~(1u << i);
-      } else if (fresh(w[i])) {
-        v[i] = w[i];
-        stale &= ~(1u << i);
-      }
-    }
-    polls = 2;
-    spin = 2;
-  }
   if (__any(stale != 0)) {
-    for (;; ++spin) {
+    if constexpr (DELAY > 0) __builtin_amdgcn_s_sleep(DELAY);
+    for (int spin = 0;; ++spin) {
 #pragma unroll
       for (int i = 0; i < NPT; ++i)
         if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
@@ -749,7 +730,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(3);
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(1), true>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
                                       p.force_giveup ? ltag % 65535u + 1u : ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 1>{});
                                       })) {
@@ -785,7 +766,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(6);
   }
   barrier_lds();
-  if (!gather_b<M, I, G::ks(2), false>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
+  if (!gather_b<M, I, G::ks(2), false, 0>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
                                        p.spin_limit, p.eps, polls, [&] {
         prime(std::integral_constant<int, 2>{});
       })) {
@@ -816,7 +797,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     return;
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(3), true>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
                                       ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 3>{});
                                       })) {
