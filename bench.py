@@ -281,20 +281,22 @@ def layer_chain(layers, x0, attn, norms, rope, mode):
     return step
 
 
-def decode_chain(layers, x0, attn, norms, rope, m):
+def decode_chain(layers, x0, attn, norms, rope, m, persistent=None):
     """The headline decode sweep: the linear path of one decode step through
     every layer, each stage data-dependent on the one before (attention
     output fixed, engine/model.py:165-190): layer 0's norm -> q|k|v (+ bias)
     -> RoPE, then per layer o + residual -> norm -> gate|up -> down +
-    residual -> the next layer's norm -> q|k|v -> RoPE.  Where a single-launch
-    configuration exists (pageserve_amd.span) each layer's part between two
-    attention calls is one persistent launch; otherwise the per-projection
-    kernels.  Returns (step, algorithmic bytes, launches, single_launch)."""
+    residual -> the next layer's norm -> q|k|v -> RoPE.  Where
+    pageserve_amd.span picks it (``persistent`` as in decode_span) each
+    layer's part between two attention calls is one persistent launch;
+    otherwise the per-projection kernels.  Returns (step, algorithmic bytes,
+    launches, single_launch)."""
     from pageserve_amd import quantization as Q
     from pageserve_amd import span as S
 
     cos, sin = rope
-    single = S.span_supported(m, HIDDEN, INTER, HIDDEN, KV, 128)
+    sizes = (m, HIDDEN, INTER, HIDDEN, KV, 128)
+    single = S.span_supported(*sizes) and (persistent is True or (persistent is None and S.span_default(*sizes)))
 
     def step():
         L0 = layers[0]
@@ -307,7 +309,8 @@ def decode_chain(layers, x0, attn, norms, rope, m):
             N = layers[i + 1] if i + 1 < len(layers) else None
             kw = {} if N is None else dict(next_ln=norms[i + 1][0], next_qkv=(N["q"], N["k"], N["v"]),
                                            next_bias=(N["q_b"], N["k_b"], N["v_b"]), cos=cos, sin=sin)
-            x, qkv = S.decode_span(attn, x, L["o"], norms[i][1], L["gate"], L["up"], L["down"], 1e-6, **kw)
+            x, qkv = S.decode_span(attn, x, L["o"], norms[i][1], L["gate"], L["up"], L["down"], 1e-6,
+                                   persistent=persistent, **kw)
             if qkv is not None:
                 outs = list(qkv)
         return [x] + outs
@@ -758,7 +761,7 @@ def counter_summary(pmc_dir, plan_path, command):
 
 def other_configs(layers, dev, steps, gate_inputs=None):
     """The remaining workload sizes, one compact figure each: decode sweeps at
-    M=4 and 16, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
+    M=4 and 16, the dependent decode chain at M=4, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
     and 512, the int8 lm_head [151936, 2048] at M=1, 8 and 256 (two copies
     alternated so the 256 MB MALL cannot hold the weight), and the single
     [4864, 896] linear at M=1 with the reference's CPU path beside it.  The
@@ -783,6 +786,21 @@ def other_configs(layers, dev, steps, gate_inputs=None):
         out[f"decode_sweep_m{m}"] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         del g
+    # the dependent decode chain at 4 tokens, as the headline's at one: the
+    # default (per-projection kernels at this size) and the single launch
+    m = 4
+    x0, attn = act(m, HIDDEN), act(m, HIDDEN)
+    norms, rope = chain_operands(dev, len(layers), m)
+    chain4 = {}
+    for name, pers in (("default", None), ("single_launch", True)):
+        step, nbytes, _, single = decode_chain(layers, x0, attn, norms, rope, m, persistent=pers)
+        g, _ = capture(step)
+        ms = time_graph(g, steps, 3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        chain4[name] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "single_launch_per_layer": single}
+        del g
+    out["decode_chain_m4"] = chain4
     for m in (128, 2048):
         x, xo = act(m, HIDDEN), act(m, HIDDEN)
         gate_inputs[m] = (x, xo)

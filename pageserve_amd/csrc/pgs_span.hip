@@ -898,7 +898,7 @@ extern "C" size_t pgs_w8a16_decode_span_workspace_bytes(int64_t m, int64_t hidde
 
 extern "C" int pgs_w8a16_decode_span_supported(int64_t m, int64_t hidden, int64_t inter, int64_t nq, int64_t nkv,
                                                 int64_t head_dim) {
-  return (m >= 1 && m <= 2 && hidden == Qwen25_3B::H && inter == Qwen25_3B::I && nq == Qwen25_3B::NQ &&
+  return (m >= 1 && m <= 4 && hidden == Qwen25_3B::H && inter == Qwen25_3B::I && nq == Qwen25_3B::NQ &&
           nkv == Qwen25_3B::NKV && head_dim == Qwen25_3B::HD)
              ? 1
              : 0;
@@ -1013,5 +1013,7 @@ extern "C" int pgs_w8a16_decode_span(const void* attn, const void* residual, voi
   int dev = -1;
   if (int rc = stream_device(st, &dev)) return rc;
   if (m == 1) return launch_span<Qwen25_3B, 1>(p, st, dev);
-  return launch_span<Qwen25_3B, 2>(p, st, dev);
+  if (m == 2) return launch_span<Qwen25_3B, 2>(p, st, dev);
+  if (m == 3) return launch_span<Qwen25_3B, 3>(p, st, dev);
+  return launch_span<Qwen25_3B, 4>(p, st, dev);
 }

@@ -8,12 +8,13 @@ then :165-173 of the next layer):
     x  = x1 + down_proj(silu(gate_proj(h)) * up_proj(h)),  h = rms_norm(x1)
     q, k, v = q|k|v_proj(rms_norm(x)) (+ bias), RoPE of q and k
 
-For the compiled configurations (``pgs_w8a16_decode_span_supported``: the
-Qwen2.5-3B shapes at one or two tokens) this is one persistent launch
-(``pgs_w8a16_decode_span``); otherwise the same steps run as the fused
-per-projection kernels (``linear`` with its residual epilogue,
-``rmsnorm_mlp``, ``rmsnorm_linear_group``, ``rope_qk``).  Either way every
-operation is a gfx950 kernel of this package.
+The compiled configurations (``pgs_w8a16_decode_span_supported``: the
+Qwen2.5-3B shapes at one to four tokens) can run as one persistent launch
+(``pgs_w8a16_decode_span``); by default the launch is used where it is the
+faster way (:func:`span_default`: one token), and otherwise the same steps
+run as the fused per-projection kernels (``linear`` with its residual
+epilogue, ``rmsnorm_mlp``, ``rmsnorm_linear_group``, ``rope_qk``).  Either way
+every operation is a gfx950 kernel of this package.
 """
 
 from __future__ import annotations
@@ -27,7 +28,7 @@ from . import _native
 from . import quantization as Q
 from ._native import LinearOut, SpanNext, SpanWeights, check
 
-__all__ = ["decode_span", "decode_span_status", "decode_span_trace", "span_supported", "TRACE_MARKS"]
+__all__ = ["decode_span", "decode_span_status", "decode_span_trace", "span_default", "span_supported", "TRACE_MARKS"]
 
 # Workspaces of the persistent launch (epoch, error word and exchange
 # buffers; zero before first use): one per (device, stream) for eager calls,
@@ -56,8 +57,20 @@ def _span_ws(dev: torch.device, stream: int, need: int) -> torch.Tensor:
 
 
 def span_supported(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim: int) -> bool:
-    """Whether :func:`decode_span` runs as one persistent launch for these sizes."""
+    """Whether :func:`decode_span` can run as one persistent launch for these
+    sizes (``persistent=True``)."""
     return bool(_native.load().pgs_w8a16_decode_span_supported(m, hidden, inter, nq, nkv, head_dim))
+
+
+def span_default(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim: int) -> bool:
+    """Whether :func:`decode_span` picks the persistent launch by default: where
+    it is compiled and faster than the per-projection kernels, i.e. at one
+    token.  The dependent 36-layer Qwen2.5-3B decode chain on MI355X, single
+    launch against per-projection kernels: 1 token 824-826 against 952-968 us;
+    2 / 3 / 4 tokens 976-991 / 1054-1078 / 1127-1185 against 973-980 /
+    1003-1017 / 1017-1028 us (from two tokens on every wave holds exchange
+    pieces, so no wave issues the next stage's loads before its gather)."""
+    return m == 1 and span_supported(m, hidden, inter, nq, nkv, head_dim)
 
 
 def decode_span_status(device: torch.device | None = None, reset: bool = True) -> None:
@@ -132,8 +145,9 @@ def decode_span(attn: torch.Tensor, residual: torch.Tensor, o: "Q.QuantizedWeigh
     ``x`` (the residual stream after the layer) and, with ``next_qkv``,
     ``(q, k, v)`` as ``[m, n]`` tensors; else ``(x, None)``.
 
-    ``persistent``: None picks the single launch where it is compiled; False
-    forces the per-projection kernels; True requires the single launch."""
+    ``persistent``: None picks the single launch where :func:`span_default`
+    says so; False forces the per-projection kernels; True requires the
+    single launch (any compiled configuration)."""
     if attn.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
         raise TypeError("decode_span: attn and residual must be bf16")
     if (next_qkv is None) != (next_ln is None):
@@ -156,11 +170,11 @@ def decode_span(attn: torch.Tensor, residual: torch.Tensor, o: "Q.QuantizedWeigh
         nq, nkv = wq.shape[0], wk.shape[0]
         if wv.shape[0] != nkv or any(w.shape[1] != hidden for w in (wq, wk, wv)):
             raise ValueError("decode_span: q [nq, h], k and v [nkv, h] expected")
-    fits = span_supported(m, hidden, inter, nq if next_qkv is not None else 2048,
-                          nkv if next_qkv is not None else 256, head_dim)
+    sizes = (m, hidden, inter, nq if next_qkv is not None else 2048, nkv if next_qkv is not None else 256, head_dim)
+    fits = span_supported(*sizes)
     if persistent is True and not fits:
         raise ValueError(f"decode_span: no single-launch configuration for m={m}, hidden={hidden}, inter={inter}")
-    if persistent is False or not fits:
+    if persistent is False or not fits or (persistent is None and not span_default(*sizes)):
         return _chain(attn, residual, o, ln_post, gate, up, down, eps, next_ln, next_qkv, next_bias, cos, sin,
                       head_dim)
 

@@ -86,13 +86,14 @@ def exchange(gpu, m):
     return x1, act, t1 | t2
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_span_stages_match_oracle(gpu, layer, m):
     L = layer
     assert S.span_supported(m, H, I, H, KV, HD)
+    assert S.span_default(m, H, I, H, KV, HD) == (m == 1)
     x, attn = activations(310 + m, m, H), activations(320 + m, m, H)
     xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
-    x_out, (q, k, v) = run_span(L, at, xt)
+    x_out, (q, k, v) = run_span(L, at, xt, persistent=True)
     torch.cuda.synchronize()
     S.decode_span_status(gpu)
     assert "launch_span" in _native.last_plan()
@@ -112,7 +113,7 @@ def test_span_stages_match_oracle(gpu, layer, m):
         report(to_np(y), O.linear(h1, qq, ss, b), H, f"m={m} {nm}", acc=O.acc_bound(h1, qq, ss, b, dx=dh1))
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_span_rope_equals_rope_of_its_projection(gpu, layer, m):
     """The RoPE in the q|k|v epilogue equals the RoPE kernel (and the oracle's
     RoPE) of the same launch's un-rotated q and k, bit for bit; v is not
@@ -120,8 +121,8 @@ def test_span_rope_equals_rope_of_its_projection(gpu, layer, m):
     x, attn = activations(330 + m, m, H), activations(340 + m, m, H)
     xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
     cos, sin = rope_tables(m)
-    x0, (q0, k0, v0) = run_span(layer, at, xt)
-    x1, (q1, k1, v1) = run_span(layer, at, xt, bf16_gpu(cos, gpu), bf16_gpu(sin, gpu))
+    x0, (q0, k0, v0) = run_span(layer, at, xt, persistent=True)
+    x1, (q1, k1, v1) = run_span(layer, at, xt, bf16_gpu(cos, gpu), bf16_gpu(sin, gpu), persistent=True)
     torch.cuda.synchronize()
     assert torch.equal(x0, x1) and torch.equal(v0, v1)
     for un, rot in ((q0, q1), (k0, k1)):
@@ -261,9 +262,9 @@ def test_span_giveup_reports_timeout_and_recovers(gpu, layer, native_lib):
 
 
 def test_span_without_configuration_runs_the_projection_kernels(gpu, layer):
-    """Four tokens have no single-launch configuration: decode_span runs the
+    """Five tokens have no single-launch configuration: decode_span runs the
     per-projection kernels, exactly the explicit chain."""
-    m = 4
+    m = 5
     assert not S.span_supported(m, H, I, H, KV, HD)
     x, attn = activations(380, m, H), activations(381, m, H)
     xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
@@ -279,3 +280,27 @@ def test_span_without_configuration_runs_the_projection_kernels(gpu, layer):
     torch.cuda.synchronize()
     for a, b in ((xs, xr), (q, qr), (k, kr), (v, vr)):
         assert torch.equal(a, b)
+
+
+def test_span_default_is_the_single_launch_at_one_token_only(gpu, layer):
+    """The single launch is compiled for 1..4 tokens and picked by default at
+    one token only (from two tokens on the per-projection kernels are as fast
+    or faster); persistent=None then runs exactly the per-projection chain,
+    and persistent=True the single launch."""
+    m = 2
+    assert S.span_supported(m, H, I, H, KV, HD) and not S.span_default(m, H, I, H, KV, HD)
+    assert S.span_default(1, H, I, H, KV, HD)
+    x, attn = activations(390, m, H), activations(391, m, H)
+    xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
+    xd, (qd, kd, vd) = run_span(layer, at, xt)
+    assert "launch_span" not in _native.last_plan()
+    xc, (qc, kc, vc) = run_span(layer, at, xt, persistent=False)
+    xs, _ = run_span(layer, at, xt, persistent=True)
+    assert "launch_span" in _native.last_plan()
+    torch.cuda.synchronize()
+    S.decode_span_status(gpu)
+    for a, b in ((xd, xc), (qd, qc), (kd, kc), (vd, vc)):
+        assert torch.equal(a, b)
+    ref = to_np(xc)
+    d = np.abs(to_np(xs) - ref)
+    assert d.max() <= 4 * O.bf16_ulp(ref).max() + O.abs_tol(I), d.max()
