@@ -99,10 +99,18 @@ constexpr int kSpanRingDefault = 4;
 // become visible needs no second in most workgroups, and reads the exchange
 // once (per step 822-824 against 846 us with two polls 16 units apart; 20 /
 // 24 / 32 units: 825 / 825 / 823 us).  The waves without pieces do not wait:
-// they issue the next stage's first loads at once.  The activation gather
-// (44 KiB per workgroup, pieces in every wave) polls at once (a delay of 16 /
-// 24 / 32 units: +1 / +5 / +10 us per step).
+// they issue the next stage's first loads at once.
 constexpr int kNormPollDelay = 28;
+// The activation gather at one token (44 KiB per workgroup) likewise: its
+// pieces in waves 0..10 (4 per thread), which poll first kActPollDelay
+// units after the publish, while waves 11..15 issue down_proj's first loads
+// at once (per step 807 against 825 us with the pieces in all 16 waves and
+// an immediate poll; 640 / 768 / 832 holding threads: 809 / 811 / 822 us; a
+// delay of 16 / 20 / 32 units: 810 / 808 / 814 us at 704 or 768 threads;
+// either change alone gains nothing).  At more tokens every wave holds
+// pieces and polls at once.
+constexpr int kActHolders = 704;
+constexpr int kActPollDelay = 24;
 constexpr int kSlot = 128;                        // exchange bytes per 8-row unit (8 rows x <= 4 tokens x 4 B)
 constexpr int kHeader = 256;                      // workspace header: [0] epoch, [1] error word
 constexpr int kSC1 = 16;                          // cache policy: sc1 (agent scope)
@@ -300,28 +308,32 @@ __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to
 
 // Gathers every unit's tagged outputs of one exchange buffer and builds the
 // next stage's B operand from them (all waves of the workgroup).  Thread
-// `tid` polls pieces tid + 1024 i (16 bytes: four words of one unit's
-// outputs of one token) into registers with agent-scope loads; a poll
-// refetches only the pieces whose tags were stale, and the workgroup stops
-// polling once no thread holds a stale piece.  A CU's vector memory
-// requests are served in order, so a poll waits behind whatever the CU has
-// queued: spreading it over all 16 waves keeps each wave's share short.
+// `tid` < HT polls pieces tid + HT i (16 bytes: four words of one unit's
+// outputs of one token) into registers with agent-scope loads, the first
+// poll DELAY s_sleep units after the workgroup's publish; a poll refetches
+// only the pieces whose tags were stale, and the workgroup stops polling
+// once no thread holds a stale piece.  A CU's vector memory requests are
+// served in order, so a poll waits behind whatever the CU has queued; the
+// waves without pieces issue the next stage's first loads at once.
 // Then, NORM: rms_norm (engine/model.py:29-34) with the norm weight in LDS,
 // r = 1 / sqrt(mean(x^2) + eps), h = bf16(w * bf16(x * r)), the sum of
 // squares in a fixed order (per thread over its pieces, a wave butterfly,
 // the 16 waves in order); otherwise the values as they are.  The B operand
 // is [M][KS] bf16 in LDS.  Returns false (the same for every thread) after
 // spin_limit polls.
-template <int M, int K, int KS, bool NORM, int DELAY, class OnPoll>
+template <int M, int K, int KS, bool NORM, int DELAY, int HT, class OnPoll>
 __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* smem, int off_b, int off_ln,
                                          int off_ssq, int* any_words, int& seq, uint32_t want, int spin_limit,
                                          float eps, int& polls, OnPoll&& on_poll) {
-  constexpr int NP = (K / 8) * 2 * M, NPT = cdiv(NP, kSpanThreads);
+  constexpr int NP = (K / 8) * 2 * M, NPT = cdiv(NP, HT);
+  static_assert(HT % 64 == 0 && HT <= kSpanThreads, "pieces held by whole waves");
   static_assert(NPT <= 32, "one stale bit per piece");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(xbuf, static_cast<int64_t>(K / 8) * kSlot);
+  // piece i of this thread (NP: none): the first HT threads hold them
+  auto piece = [&](int i) { return tid < HT ? cmin(tid + HT * i, NP) : NP; };
   auto piece_off = [&](int i) {
-    const int pc = tid + kSpanThreads * i;
+    const int pc = piece(i);
     return pc < NP ? (pc / (2 * M)) * kSlot + (pc % (2 * M)) * 16 : 0x7ffffff0;
   };
   auto fresh = [&](const u32x4& x) {
@@ -337,7 +349,7 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
   uint32_t stale = 0;
 #pragma unroll
   for (int i = 0; i < NPT; ++i)
-    if (tid + kSpanThreads * i < NP) stale |= 1u << i;
+    if (piece(i) < NP) stale |= 1u << i;
   if (__any(stale != 0)) {
     if constexpr (DELAY > 0) __builtin_amdgcn_s_sleep(DELAY);
     for (int spin = 0;; ++spin) {
@@ -364,7 +376,7 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
     for (int t = 0; t < M; ++t) ss[t] = 0.f;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      const int pc = tid + kSpanThreads * i;
+      const int pc = piece(i);
       const int t = (pc % (2 * M)) / 2;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -395,7 +407,7 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
   }
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
-    const int pc = tid + kSpanThreads * i;
+    const int pc = piece(i);
     if (pc >= NP) continue;
     const int t = (pc % (2 * M)) / 2, n0 = (pc / (2 * M)) * 8 + (pc % 2) * 4;
     u32x2 out;
@@ -730,7 +742,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(3);
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay, kSpanThreads>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
                                       p.force_giveup ? ltag % 65535u + 1u : ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 1>{});
                                       })) {
@@ -766,7 +778,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(6);
   }
   barrier_lds();
-  if (!gather_b<M, I, G::ks(2), false, 0>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
+  if (!gather_b<M, I, G::ks(2), false, M == 1 ? kActPollDelay : 0, M == 1 ? kActHolders : kSpanThreads>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
                                        p.spin_limit, p.eps, polls, [&] {
         prime(std::integral_constant<int, 2>{});
       })) {
@@ -797,7 +809,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     return;
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay, kSpanThreads>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
                                       ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 3>{});
                                       })) {
