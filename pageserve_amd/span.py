@@ -67,7 +67,7 @@ def span_default(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim: i
     it is compiled and faster than the per-projection kernels, i.e. at one
     token.  The dependent 36-layer Qwen2.5-3B decode chain on MI355X, single
     launch against per-projection kernels: 1 token 824-826 against 952-968 us;
-    2 / 3 / 4 tokens 976-991 / 1054-1078 / 1127-1185 against 973-980 /
+    2 / 3 / 4 tokens 976-991 / 1054-1078 / 1127-1185 against 960-980 /
     1003-1017 / 1017-1028 us (from two tokens on every wave holds exchange
     pieces, so no wave issues the next stage's loads before its gather)."""
     return m == 1 and span_supported(m, hidden, inter, nq, nkv, head_dim)
