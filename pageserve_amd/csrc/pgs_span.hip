@@ -360,8 +360,10 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
       for (int i = 0; i < NPT; ++i)
         if ((stale & (1u << i)) && fresh(v[i])) stale &= ~(1u << i);
       polls = spin + 1;
+      // (the next poll goes out as soon as this one is checked: each poll
+      // waits for its own data, so the loop runs at one round trip per
+      // poll; a sleep between polls measured 1-2 us per step slower)
       if (!__any(stale != 0) || spin >= spin_limit) break;
-      __builtin_amdgcn_s_sleep(1);
     }
   }
   on_poll();
