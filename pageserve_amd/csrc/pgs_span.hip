@@ -98,7 +98,9 @@ constexpr int kSpanRingDefault = 4;
 // comes a round trip later.  One poll at about the time the last words
 // become visible needs no second in most workgroups, and reads the exchange
 // once (per step 822-824 against 846 us with two polls 16 units apart; 20 /
-// 24 / 32 units: 825 / 825 / 823 us).  The waves without pieces do not wait:
+// 24 / 32 units: 825 / 825 / 823 us; measured before the activation gather
+// below took its form, with it 24 / 26 / 30 units are within 1-2 us of 28).
+// The waves without pieces do not wait:
 // they issue the next stage's first loads at once.
 constexpr int kNormPollDelay = 28;
 // The activation gather at one token (44 KiB per workgroup) likewise: its
