@@ -11,7 +11,7 @@ then :165-173 of the next layer):
 The compiled configurations (``pgs_w8a16_decode_span_supported``: the
 Qwen2.5-3B shapes at one to four tokens) can run as one persistent launch
 (``pgs_w8a16_decode_span``); by default the launch is used where it is the
-faster way (:func:`span_default`: one token), and otherwise the same steps
+faster way (:func:`span_default`: one and two tokens), and otherwise the same steps
 run as the fused per-projection kernels (``linear`` with its residual
 epilogue, ``rmsnorm_mlp``, ``rmsnorm_linear_group``, ``rope_qk``).  Either way
 every operation is a gfx950 kernel of this package.
@@ -64,13 +64,13 @@ def span_supported(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim:
 
 def span_default(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim: int) -> bool:
     """Whether :func:`decode_span` picks the persistent launch by default: where
-    it is compiled and faster than the per-projection kernels, i.e. at one
-    token.  The dependent 36-layer Qwen2.5-3B decode chain on MI355X, single
-    launch against per-projection kernels: 1 token 824-826 against 952-968 us;
-    2 / 3 / 4 tokens 976-991 / 1054-1078 / 1127-1185 against 960-980 /
-    1003-1017 / 1017-1028 us (from two tokens on every wave holds exchange
-    pieces, so no wave issues the next stage's loads before its gather)."""
-    return m == 1 and span_supported(m, hidden, inter, nq, nkv, head_dim)
+    it is compiled and faster than the per-projection kernels, i.e. at one and
+    two tokens.  The dependent 36-layer Qwen2.5-3B decode chain on MI355X,
+    single launch against per-projection kernels: 1 / 2 / 3 / 4 tokens 793 /
+    944 / 1040 / 1120 against 963 / 963 / 1005 / 1016 us (from two tokens on
+    every wave holds exchange pieces, so no wave issues the next stage's loads
+    before its gather)."""
+    return m <= 2 and span_supported(m, hidden, inter, nq, nkv, head_dim)
 
 
 def decode_span_status(device: torch.device | None = None, reset: bool = True) -> None:

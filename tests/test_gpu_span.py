@@ -90,7 +90,7 @@ def exchange(gpu, m):
 def test_span_stages_match_oracle(gpu, layer, m):
     L = layer
     assert S.span_supported(m, H, I, H, KV, HD)
-    assert S.span_default(m, H, I, H, KV, HD) == (m == 1)
+    assert S.span_default(m, H, I, H, KV, HD) == (m <= 2)
     x, attn = activations(310 + m, m, H), activations(320 + m, m, H)
     xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
     x_out, (q, k, v) = run_span(L, at, xt, persistent=True)
@@ -282,14 +282,14 @@ def test_span_without_configuration_runs_the_projection_kernels(gpu, layer):
         assert torch.equal(a, b)
 
 
-def test_span_default_is_the_single_launch_at_one_token_only(gpu, layer):
+def test_span_default_is_the_single_launch_at_one_and_two_tokens_only(gpu, layer):
     """The single launch is compiled for 1..4 tokens and picked by default at
-    one token only (from two tokens on the per-projection kernels are as fast
-    or faster); persistent=None then runs exactly the per-projection chain,
+    one and two tokens only (from three tokens on the per-projection kernels
+    are faster); persistent=None then runs exactly the per-projection chain,
     and persistent=True the single launch."""
-    m = 2
+    m = 3
     assert S.span_supported(m, H, I, H, KV, HD) and not S.span_default(m, H, I, H, KV, HD)
-    assert S.span_default(1, H, I, H, KV, HD)
+    assert S.span_default(1, H, I, H, KV, HD) and S.span_default(2, H, I, H, KV, HD)
     x, attn = activations(390, m, H), activations(391, m, H)
     xt, at = bf16_gpu(x, gpu), bf16_gpu(attn, gpu)
     xd, (qd, kd, vd) = run_span(layer, at, xt)
