@@ -323,7 +323,7 @@ __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to
 // the 16 waves in order); otherwise the values as they are.  The B operand
 // is [M][KS] bf16 in LDS.  Returns false (the same for every thread) after
 // spin_limit polls.
-template <int M, int K, int KS, bool NORM, int DELAY, int HT, class OnPoll>
+template <int M, int K, int KS, bool NORM, int DELAY, int HT, bool EARLY, class OnPoll>
 __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* smem, int off_b, int off_ln,
                                          int off_ssq, int* any_words, int& seq, uint32_t want, int spin_limit,
                                          float eps, int& polls, OnPoll&& on_poll) {
@@ -345,19 +345,27 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
   // pieces waits DELAY s_sleep units before its first poll), and only then
   // issues (on_poll) the next stage's first loads: a wave's loads return in
   // order, so a poll issued behind its own weight loads would wait for
-  // them.  Then the workgroup-wide check (which also makes a give-up
-  // uniform).
+  // them.  EARLY: a holding wave issues them right behind its first poll
+  // instead, which still returns first; only a second poll then waits
+  // behind them (the normalising gathers at one token, where the median
+  // workgroup polls once: per step 786-787 against 792-793 us; x1 alone
+  // 791; the activation gather too: 810).  Then the workgroup-wide check
+  // (which also makes a give-up uniform).
   u32x4 v[NPT];
   uint32_t stale = 0;
 #pragma unroll
   for (int i = 0; i < NPT; ++i)
     if (piece(i) < NP) stale |= 1u << i;
-  if (__any(stale != 0)) {
+  const bool holder = __any(stale != 0);
+  if (holder) {
     if constexpr (DELAY > 0) __builtin_amdgcn_s_sleep(DELAY);
     for (int spin = 0;; ++spin) {
 #pragma unroll
       for (int i = 0; i < NPT; ++i)
         if (stale & (1u << i)) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, piece_off(i), 0, kSC1);
+      if constexpr (EARLY) {
+        if (spin == 0) on_poll();
+      }
 #pragma unroll
       for (int i = 0; i < NPT; ++i)
         if ((stale & (1u << i)) && fresh(v[i])) stale &= ~(1u << i);
@@ -368,7 +376,7 @@ __device__ __forceinline__ bool gather_b(const uint32_t* xbuf, unsigned char* sm
       if (!__any(stale != 0) || spin >= spin_limit) break;
     }
   }
-  on_poll();
+  if (!EARLY || !holder) on_poll();
   // piece pc: unit pc / 2M (rows 8 unit ..), token (pc % 2M) / 2, rows
   // 8 unit + 4 (pc % 2) + e for its words e = 0..3
   // NORM: each wave's sum of squares goes to LDS before the workgroup-wide
@@ -752,7 +760,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(3);
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay, kSpanThreads>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay, kSpanThreads, M == 1>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
                                       p.force_giveup ? ltag % 65535u + 1u : ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 1>{});
                                       })) {
@@ -788,7 +796,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(6);
   }
   barrier_lds();
-  if (!gather_b<M, I, G::ks(2), false, M == 1 ? kActPollDelay : 0, M == 1 ? kActHolders : kSpanThreads>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
+  if (!gather_b<M, I, G::ks(2), false, M == 1 ? kActPollDelay : 0, M == 1 ? kActHolders : kSpanThreads, false>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
                                        p.spin_limit, p.eps, polls, [&] {
         prime(std::integral_constant<int, 2>{});
       })) {
@@ -819,7 +827,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     return;
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay, kSpanThreads>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay, kSpanThreads, M == 1>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
                                       ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 3>{});
                                       })) {
