@@ -222,3 +222,21 @@ def test_host_module_loads_and_matches_the_abi(native_lib):
     host = _native.load_host()
     assert host.abi_version() == _native.ABI_VERSION
     assert callable(host.linear) and callable(host.swiglu)
+
+
+def test_span_configurations_and_default(native_lib):
+    """The persistent decode span is compiled for the Qwen2.5-3B shapes at 1..4
+    tokens (its workspace is sized for them) and is the default path of
+    decode_span at one and two tokens only; other sizes run the
+    per-projection kernels."""
+    from pageserve_amd import span as S
+
+    qwen = (2048, 11008, 2048, 256, 128)
+    for m in range(0, 7):
+        assert S.span_supported(m, *qwen) == (1 <= m <= 4), m
+        assert S.span_default(m, *qwen) == (1 <= m <= 2), m
+    assert not S.span_supported(1, 2048, 11008, 2048, 256, 64)
+    assert not S.span_supported(1, 4096, 11008, 2048, 256, 128)
+    ws = native_lib.pgs_w8a16_decode_span_workspace_bytes
+    assert ws(1, 2048, 11008) == ws(4, 2048, 11008) > 0
+    assert ws(5, 2048, 11008) == 0 and ws(0, 2048, 11008) == 0
