@@ -347,7 +347,7 @@ def span_timeline(dev, layers_n, m, command):
     x = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
     xo = torch.randn((m, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
     norms, rope = chain_operands(dev, layers_n, m)
-    step, _, _, single = decode_chain(layers, x, xo, norms, rope, m)
+    step, _, _, single = decode_chain(layers, x, xo, norms, rope, m, persistent=True)
     if not single:
         raise SystemExit(f"bench.py: no single-launch decode span at m={m}")
     plain, _ = capture(step)
