@@ -109,8 +109,9 @@ constexpr int kNormPollDelay = 28;
 // at once (per step 807 against 825 us with the pieces in all 16 waves and
 // an immediate poll; 640 / 768 / 832 holding threads: 809 / 811 / 822 us; a
 // delay of 16 / 20 / 32 units: 810 / 808 / 814 us at 704 or 768 threads;
-// either change alone gains nothing).  At more tokens every wave holds
-// pieces and polls at once.
+// either change alone gains nothing).  The same at two tokens (8 pieces
+// per thread; the two-token chain 932 against 946 us); at three and four
+// every wave holds pieces and polls at once.
 constexpr int kActHolders = 704;
 constexpr int kActPollDelay = 24;
 constexpr int kSlot = 128;                        // exchange bytes per 8-row unit (8 rows x <= 4 tokens x 4 B)
@@ -796,7 +797,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(6);
   }
   barrier_lds();
-  if (!gather_b<M, I, G::ks(2), false, M == 1 ? kActPollDelay : 0, M == 1 ? kActHolders : kSpanThreads, false>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
+  if (!gather_b<M, I, G::ks(2), false, M <= 2 ? kActPollDelay : 0, M <= 2 ? kActHolders : kSpanThreads, false>(actx, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq, ltag,
                                        p.spin_limit, p.eps, polls, [&] {
         prime(std::integral_constant<int, 2>{});
       })) {
