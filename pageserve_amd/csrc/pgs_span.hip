@@ -103,6 +103,11 @@ constexpr int kSpanRingDefault = 4;
 // The waves without pieces do not wait:
 // they issue the next stage's first loads at once.
 constexpr int kNormPollDelay = 28;
+// From two tokens on every wave holds pieces and polls after a shorter
+// delay (the chain at 2 / 3 / 4 tokens with 0 / 8 / 14 / 20 / 28 units:
+// 926 / 922 / 919 / 921 / 931, 1040 / 1035 / 1031 / 1033 / 1041 and
+// 1116 / 1116 / 1111 / 1114 / 1120 us).
+constexpr int kNormPollDelayMulti = 14;
 // The activation gather at one token (44 KiB per workgroup) likewise: its
 // pieces in waves 0..10 (4 per thread), which poll first kActPollDelay
 // units after the publish, while waves 11..15 issue down_proj's first loads
@@ -761,7 +766,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     PGS_SPAN_MARK(3);
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(1), true, kNormPollDelay, kSpanThreads, M == 1>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(1), true, M == 1 ? kNormPollDelay : kNormPollDelayMulti, kSpanThreads, M == 1>(x1x, smem, G::kOffB, G::kOffLn, G::kOffSsq, flag + 4, any_seq,
                                       p.force_giveup ? ltag % 65535u + 1u : ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 1>{});
                                       })) {
@@ -828,7 +833,7 @@ __global__ __launch_bounds__(kSpanThreads, 1) void span_kernel(SpanParams p) {
     return;
   }
   barrier_lds();
-  if (!gather_b<M, H, G::ks(3), true, kNormPollDelay, kSpanThreads, M == 1>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
+  if (!gather_b<M, H, G::ks(3), true, M == 1 ? kNormPollDelay : kNormPollDelayMulti, kSpanThreads, M == 1>(x2x, smem, G::kOffB, G::kOffLn + H * 2, G::kOffSsq, flag + 4, any_seq,
                                       ltag, p.spin_limit, p.eps, polls, [&] {
                                         prime(std::integral_constant<int, 3>{});
                                       })) {

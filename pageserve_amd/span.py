@@ -67,7 +67,7 @@ def span_default(m: int, hidden: int, inter: int, nq: int, nkv: int, head_dim: i
     it is compiled and faster than the per-projection kernels, i.e. at one and
     two tokens.  The dependent 36-layer Qwen2.5-3B decode chain on MI355X,
     single launch against per-projection kernels: 1 / 2 / 3 / 4 tokens 788 /
-    932 / 1040 / 1120 against 963 / 973 / 1005 / 1016 us (from two tokens on
+    918 / 1031 / 1111 against 963 / 973 / 1005 / 1016 us (from two tokens on
     every wave holds pieces of the normed-input gathers, so no wave issues the
     next stage's loads before those gathers)."""
     return m <= 2 and span_supported(m, hidden, inter, nq, nkv, head_dim)
