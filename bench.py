@@ -761,7 +761,7 @@ def counter_summary(pmc_dir, plan_path, command):
 
 def other_configs(layers, dev, steps, gate_inputs=None):
     """The remaining workload sizes, one compact figure each: decode sweeps at
-    M=4 and 16, the dependent decode chain at M=4, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
+    M=4 and 16, the dependent decode chain at M=2 and 4, prefill sweeps at M=128 and 2048, the fused SwiGLU MLP at M=1
     and 512, the int8 lm_head [151936, 2048] at M=1, 8 and 256 (two copies
     alternated so the 256 MB MALL cannot hold the weight), and the single
     [4864, 896] linear at M=1 with the reference's CPU path beside it.  The
@@ -786,21 +786,25 @@ def other_configs(layers, dev, steps, gate_inputs=None):
         out[f"decode_sweep_m{m}"] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         del g
-    # the dependent decode chain at 4 tokens, as the headline's at one: the
-    # default (per-projection kernels at this size) and the single launch
-    m = 4
-    x0, attn = act(m, HIDDEN), act(m, HIDDEN)
-    norms, rope = chain_operands(dev, len(layers), m)
-    chain4 = {}
-    for name, pers in (("default", None), ("single_launch", True)):
-        step, nbytes, _, single = decode_chain(layers, x0, attn, norms, rope, m, persistent=pers)
-        g, _ = capture(step)
-        ms = time_graph(g, steps, 3)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        chain4[name] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "single_launch_per_layer": single}
-        del g
-    out["decode_chain_m4"] = chain4
+    from pageserve_amd import span as S
+
+    # the dependent decode chain at 2 and 4 tokens, as the headline's at one:
+    # the single launch and the per-projection kernels, and which of the two
+    # decode_span picks by default at that size
+    for m in (2, 4):
+        x0, attn = act(m, HIDDEN), act(m, HIDDEN)
+        norms, rope = chain_operands(dev, len(layers), m)
+        chain = {"default": "single_launch" if S.span_default(m, HIDDEN, INTER, HIDDEN, KV, 128)
+                 else "per_projection"}
+        for name, pers in (("single_launch", True), ("per_projection", False)):
+            step, nbytes, _, single = decode_chain(layers, x0, attn, norms, rope, m, persistent=pers)
+            g, _ = capture(step)
+            ms = time_graph(g, steps, 3)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            chain[name] = {"us_per_sweep": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "single_launch_per_layer": single}
+            del g
+        out[f"decode_chain_m{m}"] = chain
     for m in (128, 2048):
         x, xo = act(m, HIDDEN), act(m, HIDDEN)
         gate_inputs[m] = (x, xo)
